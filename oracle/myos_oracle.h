@@ -1,0 +1,106 @@
+/*
+ * CPU oracle for the batch-1 BF16-weight / FP32-accumulate token loop.
+ *
+ * TEST INFRASTRUCTURE ONLY. This is a restatement of the reference's CPU
+ * path (crates/tensor_core and crates/model_core), kept bit-faithful: every
+ * f32 operation is one IEEE rounding in the reference's order, products are
+ * formed before they are added (built with -ffp-contract=off), and the
+ * transcendental functions are the same glibc libm entry points the reference
+ * links (sqrtf, expf, powf, sinf, cosf). It is used by tests/, by the smoke
+ * check and as the bench's CPU baseline. The product path never links it.
+ *
+ * Parity pins (what fixes each function independently of this file):
+ *   orc_bf16_to_f32          bf16.rs:316-320 known bits
+ *   orc_gemv_bf16(_mt)       bf16.rs:350-362 hand values; gemv_bf16_kernel.rs:929-951
+ *                            2^24 cancellation order; AVX2 == scalar bit-equality;
+ *                            brute-force f64 error bound
+ *   orc_add_bf16_bias        bf16.rs:324-347 hand values
+ *   orc_embed_gather_bf16    bf16.rs:381-396 hand values
+ *   orc_rmsnorm_bf16_weight  bf16.rs:311,488-544 bits (eps, serial order, 0x3f7ffff8)
+ *   orc_rope_*               rope.rs:230-360 bits
+ *   orc_gqa_attn_f32         gqa.rs:357-608 bits
+ *   orc_silu_f32 / swiglu    swiglu.rs:362-452 bits
+ *   orc_greedy_token         model_core/src/lib.rs:157-167 spec (ties, NaN)
+ *   orc_model_*              qwen25_block.rs:1011-1071 block fixture [1,2,0,-1] / [1,1,1,1];
+ *                            :1423-1478 chunk prefill == serial forward bits
+ */
+#ifndef MYOS_ORACLE_H
+#define MYOS_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* status codes mirror the reference error enums (one code per variant) */
+enum {
+  ORC_OK = 0,
+  ORC_E_SHAPE = 1,
+  ORC_E_TOKEN = 2,
+  ORC_E_ROW_OOB = 3,
+  ORC_E_POSITION = 4,
+  ORC_E_KV_FULL = 5,
+  ORC_E_KV_RANGE = 6,
+};
+
+float orc_bf16_to_f32(uint16_t bits);
+
+/* tensor_core ops (reference semantics, host pointers) */
+int orc_gemv_bf16(float *y, const uint16_t *w, const float *x, size_t m, size_t k);
+int orc_gemv_bf16_mt(float *y, const uint16_t *w, const float *x, size_t m, size_t k,
+                     int threads);
+int orc_gemm_bf16_mt(float *y, const uint16_t *w, const float *x, size_t batch, size_t m,
+                     size_t k, int threads);
+void orc_add_bf16_bias(float *y, const uint16_t *bias, size_t n);
+int orc_embed_gather_bf16(float *out, const uint16_t *table, size_t vocab, size_t hidden,
+                          uint32_t token);
+int orc_rmsnorm_bf16_weight(float *y, const uint16_t *gamma, const float *x, size_t n,
+                            float eps);
+int orc_rope_inv_freqs(float *inv_freq, size_t head_dim, float theta);
+int orc_rope_f32_inplace(float *x, size_t len, uint32_t position, size_t head_dim,
+                         float theta);
+float orc_attn_scale_f32(size_t head_dim);
+/* mask: 0 = Full, 1 = Causal{query_pos} */
+int orc_gqa_attn_f32(float *y, const float *q, const float *k, const float *v, float *probs,
+                     size_t nq, size_t nkv, size_t head_dim, size_t seq, int mask,
+                     size_t query_pos);
+float orc_silu_f32(float z);
+void orc_swiglu_mul_f32(float *h, const float *gate, const float *up, size_t n);
+uint32_t orc_greedy_token(const float *logits, size_t n);
+
+/* model_core: one Qwen2.5-shaped decoder over caller-owned BF16 weights */
+typedef struct {
+  size_t hidden, num_q_heads, num_kv_heads, head_dim, intermediate, vocab, num_layers;
+  float rms_eps, rope_theta;
+} orc_shape;
+
+typedef struct {
+  const uint16_t *ln1, *wq, *bq, *wk, *bk, *wv, *bv, *wo, *ln2, *wg, *wu, *wd;
+} orc_layer;
+
+typedef struct orc_model orc_model;
+
+/* lm_head == NULL means the head is tied to embed (the reference's only form) */
+orc_model *orc_model_new(const orc_shape *shape, size_t max_seq, const orc_layer *layers,
+                         const uint16_t *embed, const uint16_t *final_norm,
+                         const uint16_t *lm_head, int threads);
+void orc_model_free(orc_model *m);
+int orc_forward_token(orc_model *m, uint32_t token, size_t pos);
+int orc_prefill(orc_model *m, const uint32_t *tokens, size_t n);
+int orc_greedy_decode(orc_model *m, size_t steps, uint32_t *out);
+size_t orc_cache_len(const orc_model *m);
+const float *orc_logits(const orc_model *m);
+const float *orc_hidden(const orc_model *m);  /* residual stream after the last layer */
+const float *orc_normed(const orc_model *m);  /* final-norm output fed to the head */
+int orc_kv_read(const orc_model *m, size_t layer, size_t head, size_t pos, float *k, float *v);
+void orc_set_threads(orc_model *m, int threads);
+int orc_attention_layer(orc_model *m, size_t layer, size_t pos, float *residual,
+                        const float *proj_in);
+int orc_kv_advance(orc_model *m);
+
+#ifdef __cplusplus
+}
+#endif
+#endif
