@@ -1,0 +1,125 @@
+// Internal launcher API between the kernel translation unit (myos_kernels.hip)
+// and the host code (op tier, model tier). Not part of the C ABI.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace myos {
+
+// ---- GEMV family: one launch streams a row-major BF16 matrix once ----------
+enum GemvX { X_PLAIN = 0, X_NORM = 1 };
+enum GemvEpi { EPI_STORE = 0, EPI_RESID = 1, EPI_QKV = 2, EPI_GU = 3, EPI_HEAD = 4 };
+
+struct GemvArgs {
+  const uint16_t *w = nullptr;  // [m, k]
+  const float *x = nullptr;     // [k]
+  const uint16_t *gamma = nullptr;  // X_NORM gains [k]
+  float eps = 0.f;
+  int m = 0, k = 0;
+  float *y = nullptr;           // STORE/HEAD: out[m]; RESID: residual[m] += row
+  float *normed_out = nullptr;  // X_NORM: block 0 also writes the normed vector here
+  // EPI_QKV: rows permuted so RoPE pairs (p, p + d/2) are adjacent
+  const float *bias = nullptr;  // f32 [m] in the permuted row order
+  const float2 *rope = nullptr; // [max_seq][d/2] (cos, sin)
+  const uint32_t *pos_ptr = nullptr;  // device position (decode state)
+  float *q_out = nullptr;       // [q_dim], natural order
+  void *kc = nullptr, *vc = nullptr;  // this layer's cache [nkv][max_seq][d]
+  int kv_bf16 = 0, max_seq = 0, q_dim = 0, kv_dim = 0, head_dim = 0;
+  // EPI_GU: rows (2i, 2i+1) = (gate_i, up_i); h[i] = silu(gate_i) * up_i
+  float *h_out = nullptr;
+  // EPI_HEAD: per-block (value, index) argmax partials
+  float2 *part = nullptr;       // x = value, y = index bits
+  uint32_t *pos_inc = nullptr;  // EPI_HEAD: block 0 increments *pos_inc when set
+};
+
+// Launch the best kernel variant for (m, k, x mode, epilogue); returns the
+// number of argmax partials written (EPI_HEAD) or 0.
+hipError_t launch_gemv(const GemvArgs &a, GemvX xm, GemvEpi epi, hipStream_t s,
+                       int *n_parts = nullptr);
+int gemv_head_parts(int m, int k);  // partial count EPI_HEAD will produce
+
+// ---- decode attention over the HBM cache (split positions + last-block merge)
+struct AttnDecodeArgs {
+  const float *q;          // [nq, d] (RoPE applied)
+  const void *kc, *vc;     // this layer's cache [nkv][max_seq][d]
+  int kv_bf16, max_seq, nq, nkv, head_dim;
+  const uint32_t *pos_ptr; // attends positions 0..*pos_ptr
+  float *part;             // scratch [nq][nchunks][d + 2]
+  unsigned *counters;      // [nkv], zero at rest (the merging block resets it)
+  float *out;              // [nq, d]
+};
+int attn_decode_chunks(int max_seq);
+size_t attn_decode_part_floats(int nq, int max_seq, int head_dim);
+hipError_t launch_attn_decode(const AttnDecodeArgs &a, hipStream_t s);
+
+// ---- small ops --------------------------------------------------------------
+hipError_t launch_fill_zero(float *y, size_t n, hipStream_t s);
+hipError_t launch_add_bias(float *y, const uint16_t *b, size_t n, hipStream_t s);
+hipError_t launch_embed_gather(float *out, const uint16_t *table, size_t hidden,
+                               const uint32_t *token_dev, uint32_t token_host, hipStream_t s);
+hipError_t launch_rmsnorm(float *y, const uint16_t *g, const float *x, size_t n, float eps,
+                          hipStream_t s);
+hipError_t launch_rope_apply(float *x, size_t len, size_t head_dim, const float2 *cs,
+                             hipStream_t s);
+hipError_t launch_gqa_general(float *y, const float *q, const float *k, const float *v,
+                              float *probs, float *scratch, int nq, int nkv, int d, int seq,
+                              int mask, size_t query_pos, hipStream_t s);
+hipError_t launch_swiglu_mul(float *h, const float *g, const float *u, size_t n, hipStream_t s);
+int argmax_parts(size_t n);
+hipError_t launch_argmax_partial(const float *logits, size_t n, float2 *part, hipStream_t s);
+
+// final argmax reduction; optionally also the decode-step prologue:
+// token -> state[1], out_ids[state[2]++] = token, x = embed[token]
+struct ArgmaxFinalArgs {
+  const float2 *part = nullptr;
+  int nparts = 0;
+  uint32_t *token_out = nullptr;       // plain result
+  uint32_t *state = nullptr;           // [pos, token, step, mode]; mode 1 = take state[1]
+  uint32_t *out_ids = nullptr;
+  const uint16_t *embed = nullptr;
+  float *x = nullptr;
+  int hidden = 0;
+};
+hipError_t launch_argmax_final(const ArgmaxFinalArgs &a, hipStream_t s);
+
+// ---- prefill ----------------------------------------------------------------
+hipError_t launch_embed_rows(float *X, const uint16_t *embed, const uint32_t *tokens, int M,
+                             int H, hipStream_t s);
+// rows of X -> rmsnorm -> bf16 hi/lo planes (A operand of the MFMA GEMM)
+hipError_t launch_rmsnorm_rows_split(const float *X, const uint16_t *g, float eps, int M, int H,
+                                     uint16_t *hi, uint16_t *lo, hipStream_t s);
+hipError_t launch_split_rows(const float *X, size_t n, uint16_t *hi, uint16_t *lo,
+                             hipStream_t s);
+
+struct GemmArgs {
+  const uint16_t *a_hi, *a_lo;  // [M, K] bf16 planes
+  const uint16_t *w;            // [N, K] bf16
+  int M, N, K;
+  float *y;                     // STORE: [M, N]; RESID: [M, N] +=
+  // EPI_QKV (N = q_dim + 2 kv_dim, permuted rows)
+  const float *bias;
+  const float2 *rope;
+  int start_pos;
+  float *q_out;                 // [M, q_dim]
+  void *kc, *vc;
+  int kv_bf16, max_seq, q_dim, kv_dim, head_dim;
+  // EPI_GU: writes h = silu(g)*u as hi/lo planes [M, N/2]
+  uint16_t *h_hi, *h_lo;
+};
+hipError_t launch_gemm(const GemmArgs &a, GemvEpi epi, hipStream_t s);
+
+struct AttnPrefillArgs {
+  const float *q;               // [M, nq*d]
+  const void *kc, *vc;
+  int kv_bf16, max_seq, nq, nkv, head_dim, M, start_pos;
+  uint16_t *out_hi, *out_lo;    // [M, nq*d]
+};
+hipError_t launch_attn_prefill(const AttnPrefillArgs &a, hipStream_t s);
+
+hipError_t launch_permute_rows(uint16_t *dst, const uint16_t *src, const int *perm, int rows,
+                               int cols, hipStream_t s);
+
+const char *kernel_build_info();
+
+}  // namespace myos

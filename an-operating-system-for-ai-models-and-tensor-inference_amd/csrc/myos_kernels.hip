@@ -1,0 +1,1039 @@
+// HIP kernels for the batch-1 BF16-weight / FP32-accumulate token loop on
+// MI355X (gfx950, CDNA4): 64-wide wavefronts, 256 CUs in 8 XCDs, HBM3E.
+//
+// Decode is a weight stream: every projection reads its BF16 matrix from HBM
+// exactly once per token, so each GEMV kernel is written to keep many 16-byte
+// loads in flight per lane and to fuse the surrounding elementwise work
+// (RMSNorm prologue; bias + RoPE + KV-store, SwiGLU, residual and argmax
+// epilogues) so no activation round-trips through HBM between launches.
+// Prefill's projections run on MFMA (v_mfma_f32_32x32x16_bf16).
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+
+#include "myos_internal.h"
+
+namespace myos {
+namespace {
+
+constexpr int kWave = 64;
+constexpr int kBlock = 256;
+
+__device__ __forceinline__ float bf_lo(uint32_t v) { return __uint_as_float(v << 16); }
+__device__ __forceinline__ float bf_hi(uint32_t v) { return __uint_as_float(v & 0xffff0000u); }
+__device__ __forceinline__ float bf16f(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
+
+// round to nearest even; NaN stays a quiet NaN
+__device__ __forceinline__ uint16_t f2bf(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+template <int W>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+  for (int o = W / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, W);
+  return v;
+}
+template <int W>
+__device__ __forceinline__ float group_max(float v) {
+#pragma unroll
+  for (int o = W / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, W));
+  return v;
+}
+
+// SiLU as the reference spells it: z / (1 + expf(-z)) (swiglu.rs:113-115)
+__device__ __forceinline__ float silu(float z) { return z / (1.0f + expf(-z)); }
+
+// greedy_token ordering (model_core/src/lib.rs:157-167): a candidate wins on a
+// strictly larger value, or on an equal value at a lower index; -inf and NaN
+// never win, so an all -inf/NaN vector ends with index UINT32_MAX -> 0.
+__device__ __forceinline__ bool beats(float v, uint32_t i, float bv, uint32_t bi) {
+  return v > bv || (v == bv && v != -INFINITY && i < bi);
+}
+
+__device__ __forceinline__ float load_kv(const void *base, size_t idx, int bf16) {
+  return bf16 ? bf16f(((const uint16_t *)base)[idx]) : ((const float *)base)[idx];
+}
+__device__ __forceinline__ void store_kv(void *base, size_t idx, float v, int bf16) {
+  if (bf16)
+    ((uint16_t *)base)[idx] = f2bf(v);
+  else
+    ((float *)base)[idx] = v;
+}
+
+// Block-wide sum over 256 threads in a fixed order (wave partials, then 0..3).
+__device__ float block_sum(float v, float *scratch4) {
+  v = group_sum<kWave>(v);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane == 0) scratch4[wave] = v;
+  __syncthreads();
+  return ((scratch4[0] + scratch4[1]) + scratch4[2]) + scratch4[3];
+}
+
+// --------------------------------------------------------------- GEMV -----
+//
+// One "team" (a wavefront, TEAM = 64, or the whole 256-thread workgroup,
+// TEAM = 256) computes ROWS consecutive rows. Thread t of a team owns the
+// 8-column chunks t, t + TEAM, ... (CPT of them at most), so its slice of x
+// is loaded from LDS into registers once and reused for every row, and the
+// ROWS x CPT 16-byte weight loads are all issued before the first FMA.
+// x is staged through LDS once per workgroup; with X_NORM the workgroup also
+// applies the RMSNorm there (sum of squares over the whole vector, then
+// g * (x * inv_rms)), which fuses rmsnorm_bf16_weight into the projection.
+
+template <int XM>
+__device__ void stage_x(const GemvArgs &a, float *xs, float *red4) {
+  const int k = a.k, tid = threadIdx.x;
+  float ss = 0.f;
+  for (int j = tid * 4; j < k; j += kBlock * 4) {
+    float4 v = *(const float4 *)(a.x + j);
+    *(float4 *)(xs + j) = v;
+    if (XM == X_NORM) ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+  }
+  if (XM == X_NORM) {
+    float tot = block_sum(ss, red4);
+    float mean = tot / (float)k;
+    float inv = 1.0f / sqrtf(mean + a.eps);
+    for (int j = tid * 4; j < k; j += kBlock * 4) {
+      float4 v = *(float4 *)(xs + j);
+      uint2 g = *(const uint2 *)(a.gamma + j);
+      v.x = bf_lo(g.x) * (v.x * inv);
+      v.y = bf_hi(g.x) * (v.y * inv);
+      v.z = bf_lo(g.y) * (v.z * inv);
+      v.w = bf_hi(g.y) * (v.w * inv);
+      *(float4 *)(xs + j) = v;
+      if (a.normed_out && blockIdx.x == 0) *(float4 *)(a.normed_out + j) = v;
+    }
+  }
+  __syncthreads();
+}
+
+// Epilogue for one team's ROWS results (run by the team's thread 0).
+template <int EPI, int ROWS>
+__device__ __forceinline__ void gemv_epilogue(const GemvArgs &a, int row0, const float *v,
+                                              uint32_t pos, float2 *team_best) {
+  if (EPI == EPI_STORE) {
+#pragma unroll
+    for (int r = 0; r < ROWS; r++)
+      if (row0 + r < a.m) a.y[row0 + r] = v[r];
+  } else if (EPI == EPI_RESID) {
+#pragma unroll
+    for (int r = 0; r < ROWS; r++)
+      if (row0 + r < a.m) a.y[row0 + r] += v[r];
+  } else if (EPI == EPI_GU) {
+#pragma unroll
+    for (int r = 0; r < ROWS; r += 2)
+      if (row0 + r < a.m) a.h_out[(row0 + r) >> 1] = silu(v[r]) * v[r + 1];
+  } else if (EPI == EPI_HEAD) {
+    float bv = -INFINITY;
+    uint32_t bi = 0xffffffffu;
+#pragma unroll
+    for (int r = 0; r < ROWS; r++) {
+      int row = row0 + r;
+      if (row < a.m) {
+        a.y[row] = v[r];
+        if (beats(v[r], (uint32_t)row, bv, bi)) {
+          bv = v[r];
+          bi = (uint32_t)row;
+        }
+      }
+    }
+    *team_best = make_float2(bv, __uint_as_float(bi));
+  } else if (EPI == EPI_QKV) {
+    const int d = a.head_dim, half = d >> 1;
+#pragma unroll
+    for (int r = 0; r < ROWS; r += 2) {
+      const int row = row0 + r;
+      if (row >= a.m) break;
+      float y0 = v[r] + a.bias[row], y1 = v[r + 1] + a.bias[row + 1];
+      if (row < a.q_dim + a.kv_dim) {
+        const bool is_q = row < a.q_dim;
+        const int rr = is_q ? row : row - a.q_dim;
+        const int u = rr >> 1, head = u / half, p = u - head * half;
+        const float2 cs = a.rope[(size_t)pos * half + p];
+        const float o0 = y0 * cs.x - y1 * cs.y;
+        const float o1 = y1 * cs.x + y0 * cs.y;
+        if (is_q) {
+          a.q_out[head * d + p] = o0;
+          a.q_out[head * d + p + half] = o1;
+        } else {
+          size_t base = ((size_t)head * a.max_seq + pos) * d;
+          store_kv(a.kc, base + p, o0, a.kv_bf16);
+          store_kv(a.kc, base + p + half, o1, a.kv_bf16);
+        }
+      } else {
+        const int rr = row - a.q_dim - a.kv_dim;
+        const int head = rr / d, j = rr - head * d;
+        size_t base = ((size_t)head * a.max_seq + pos) * d + j;
+        store_kv(a.vc, base, y0, a.kv_bf16);
+        store_kv(a.vc, base + 1, y1, a.kv_bf16);
+      }
+    }
+  }
+}
+
+template <int TEAM, int ROWS, int CPT, int XM, int EPI>
+__global__ void __launch_bounds__(kBlock) gemv_kernel(GemvArgs a) {
+  extern __shared__ float4 xs4[];
+  float *xs = (float *)xs4;
+  __shared__ float red4[4];
+  __shared__ float red[4][ROWS];
+  __shared__ float2 best[4];
+  constexpr int TEAMS = kBlock / TEAM;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int team = TEAMS == 1 ? 0 : wave;
+  const int tt = TEAMS == 1 ? tid : lane;
+  const int k = a.k, m = a.m, nch = k >> 3;
+  const int row0 = (blockIdx.x * TEAMS + team) * ROWS;
+  uint32_t pos = 0;
+  if (EPI == EPI_QKV) pos = *a.pos_ptr;
+
+  // weight loads first: they do not depend on x, so they overlap the staging
+  u32x4 wv[ROWS][CPT];
+#pragma unroll
+  for (int r = 0; r < ROWS; r++) {
+    const int row = min(row0 + r, m - 1);
+    const u32x4 *rowp = (const u32x4 *)(a.w + (size_t)row * k);
+#pragma unroll
+    for (int i = 0; i < CPT; i++) {
+      const int c = tt + i * TEAM;
+      const u32x4 zero = {0u, 0u, 0u, 0u};
+      wv[r][i] = c < nch ? __builtin_nontemporal_load(rowp + c) : zero;
+    }
+  }
+
+  stage_x<XM>(a, xs, red4);
+
+  float acc[ROWS];
+#pragma unroll
+  for (int r = 0; r < ROWS; r++) acc[r] = 0.f;
+#pragma unroll
+  for (int i = 0; i < CPT; i++) {
+    const int c = tt + i * TEAM;
+    if (c < nch) {
+      const float4 x0 = xs4[c * 2], x1 = xs4[c * 2 + 1];
+#pragma unroll
+      for (int r = 0; r < ROWS; r++) {
+        const u32x4 w = wv[r][i];
+        float s = acc[r];
+        s = fmaf(bf_lo(w.x), x0.x, s);
+        s = fmaf(bf_hi(w.x), x0.y, s);
+        s = fmaf(bf_lo(w.y), x0.z, s);
+        s = fmaf(bf_hi(w.y), x0.w, s);
+        s = fmaf(bf_lo(w.z), x1.x, s);
+        s = fmaf(bf_hi(w.z), x1.y, s);
+        s = fmaf(bf_lo(w.w), x1.z, s);
+        s = fmaf(bf_hi(w.w), x1.w, s);
+        acc[r] = s;
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < ROWS; r++) acc[r] = group_sum<kWave>(acc[r]);
+  if (TEAMS == 1) {
+    if (lane == 0) {
+#pragma unroll
+      for (int r = 0; r < ROWS; r++) red[wave][r] = acc[r];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < ROWS; r++) acc[r] = ((red[0][r] + red[1][r]) + red[2][r]) + red[3][r];
+  }
+  if (tt == 0) gemv_epilogue<EPI, ROWS>(a, row0, acc, pos, &best[team]);
+  if (EPI == EPI_HEAD) {
+    __syncthreads();
+    if (tid == 0) {
+      float2 b = best[0];
+#pragma unroll
+      for (int t = 1; t < TEAMS; t++)
+        if (beats(best[t].x, __float_as_uint(best[t].y), b.x, __float_as_uint(b.y))) b = best[t];
+      a.part[blockIdx.x] = b;
+      if (blockIdx.x == 0 && a.pos_inc) *a.pos_inc += 1u;
+    }
+  }
+}
+
+// Any k (including k % 8 != 0): one wavefront per row pair, element loads.
+template <int XM, int EPI>
+__global__ void __launch_bounds__(kBlock) gemv_generic_kernel(GemvArgs a) {
+  extern __shared__ float4 xs4[];
+  float *xs = (float *)xs4;
+  __shared__ float red4[4];
+  __shared__ float2 best[4];
+  constexpr int ROWS = 2;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int k = a.k, m = a.m;
+  const int row0 = (blockIdx.x * 4 + wave) * ROWS;
+  uint32_t pos = 0;
+  if (EPI == EPI_QKV) pos = *a.pos_ptr;
+  // scalar staging (k may not be a multiple of 4)
+  float ss = 0.f;
+  for (int j = tid; j < k; j += kBlock) {
+    float v = a.x[j];
+    xs[j] = v;
+    ss += v * v;
+  }
+  if (XM == X_NORM) {
+    float tot = block_sum(ss, red4);
+    float inv = 1.0f / sqrtf(tot / (float)k + a.eps);
+    for (int j = tid; j < k; j += kBlock) {
+      float v = bf16f(a.gamma[j]) * (xs[j] * inv);
+      xs[j] = v;
+      if (a.normed_out && blockIdx.x == 0) a.normed_out[j] = v;
+    }
+  }
+  __syncthreads();
+  float acc[ROWS];
+#pragma unroll
+  for (int r = 0; r < ROWS; r++) {
+    const int row = min(row0 + r, m - 1);
+    const uint16_t *rowp = a.w + (size_t)row * k;
+    float s = 0.f;
+    for (int j = lane; j < k; j += kWave) s = fmaf(bf16f(rowp[j]), xs[j], s);
+    acc[r] = group_sum<kWave>(s);
+  }
+  if (lane == 0) gemv_epilogue<EPI, ROWS>(a, row0, acc, pos, &best[wave]);
+  if (EPI == EPI_HEAD) {
+    __syncthreads();
+    if (tid == 0) {
+      float2 b = best[0];
+      for (int t = 1; t < 4; t++)
+        if (beats(best[t].x, __float_as_uint(best[t].y), b.x, __float_as_uint(b.y))) b = best[t];
+      a.part[blockIdx.x] = b;
+      if (blockIdx.x == 0 && a.pos_inc) *a.pos_inc += 1u;
+    }
+  }
+}
+
+// ------------------------------------------------------ decode attention ---
+//
+// Workgroup (kv head g, chunk c of kAttnChunk positions) scores the chunk for
+// the q_per_kv query heads that share g (K/V read once per group), keeps a
+// chunk-local softmax (max m, sum l, unnormalised mix o), and the last
+// workgroup of the group to finish (atomic counter) merges the chunks:
+// y = sum_c e^(m_c - M) o_c / sum_c e^(m_c - M) l_c. The serial reference
+// (gqa.rs:174-218) is the same quantity with one chunk.
+constexpr int kAttnChunk = 64;
+constexpr int kMaxQPerKv = 8;
+constexpr int kMaxHeadDim = 256;
+
+__global__ void __launch_bounds__(kBlock) attn_decode_kernel(AttnDecodeArgs a) {
+  extern __shared__ float smem[];
+  const int d = a.head_dim, gq = a.nq / a.nkv, dp = d + 1;
+  float *q_s = smem;                        // [gq][d]
+  float *k_s = q_s + gq * d;                // [chunk][d + 1]
+  float *v_s = k_s + kAttnChunk * dp;       // [chunk][d]
+  float *p_s = v_s + kAttnChunk * d;        // [gq][chunk]
+  float *ml_s = p_s + gq * kAttnChunk;      // [gq][2]
+  __shared__ int is_last;
+  const int g = blockIdx.x, c = blockIdx.y, nchunks = gridDim.y, tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int seq = (int)*a.pos_ptr + 1;
+  const int t0 = c * kAttnChunk;
+  const int n = min(kAttnChunk, seq - t0);
+  const float scale = 1.0f / sqrtf((float)d);
+  const size_t stride_part = (size_t)d + 2;
+  if (n > 0) {
+    for (int i = tid; i < gq * d; i += kBlock) q_s[i] = a.q[(size_t)g * gq * d + i];
+    const size_t kv0 = ((size_t)g * a.max_seq + t0) * d;
+    for (int i = tid; i < n * d; i += kBlock) {
+      const int t = i / d, j = i - t * d;
+      k_s[t * dp + j] = load_kv(a.kc, kv0 + i, a.kv_bf16);
+      v_s[i] = load_kv(a.vc, kv0 + i, a.kv_bf16);
+    }
+    __syncthreads();
+    for (int i = tid; i < gq * n; i += kBlock) {
+      const int h = i / n, t = i - h * n;
+      const float *qh = q_s + h * d, *kt = k_s + t * dp;
+      float s = 0.f;
+      for (int j = 0; j < d; j++) s = fmaf(qh[j], kt[j], s);
+      p_s[h * kAttnChunk + t] = s * scale;
+    }
+    __syncthreads();
+    for (int h = wave; h < gq; h += 4) {
+      float s = lane < n ? p_s[h * kAttnChunk + lane] : -INFINITY;
+      const float mx = group_max<kWave>(s);
+      const float e = lane < n ? expf(s - mx) : 0.f;
+      const float l = group_sum<kWave>(e);
+      if (lane < n) p_s[h * kAttnChunk + lane] = e;
+      if (lane == 0) {
+        ml_s[2 * h] = mx;
+        ml_s[2 * h + 1] = l;
+      }
+    }
+    __syncthreads();
+    for (int i = tid; i < gq * d; i += kBlock) {
+      const int h = i / d, j = i - h * d;
+      const float *ph = p_s + h * kAttnChunk;
+      float o = 0.f;
+      for (int t = 0; t < n; t++) o = fmaf(ph[t], v_s[t * d + j], o);
+      float *dst = a.part + ((size_t)(g * gq + h) * nchunks + c) * stride_part;
+      dst[j] = o;
+      if (j == 0) {
+        dst[d] = ml_s[2 * h];
+        dst[d + 1] = ml_s[2 * h + 1];
+      }
+    }
+  }
+  // publish this chunk, elect the group's last workgroup to merge
+  __threadfence();
+  __syncthreads();
+  if (tid == 0) {
+    unsigned prev = atomicAdd(&a.counters[g], 1u);
+    is_last = prev == (unsigned)(nchunks - 1);
+  }
+  __syncthreads();
+  if (!is_last) return;
+  __threadfence();
+  const int nvalid = (seq + kAttnChunk - 1) / kAttnChunk;
+  for (int i = tid; i < gq * d; i += kBlock) {
+    const int h = i / d, j = i - h * d;
+    const float *src = a.part + (size_t)(g * gq + h) * nchunks * stride_part;
+    float mx = -INFINITY;
+    for (int cc = 0; cc < nvalid; cc++) mx = fmaxf(mx, src[cc * stride_part + d]);
+    float l = 0.f, o = 0.f;
+    for (int cc = 0; cc < nvalid; cc++) {
+      const float w = expf(src[cc * stride_part + d] - mx);
+      l = fmaf(w, src[cc * stride_part + d + 1], l);
+      o = fmaf(w, src[cc * stride_part + j], o);
+    }
+    a.out[(size_t)(g * gq + h) * d + j] = o / l;
+  }
+  if (tid == 0) a.counters[g] = 0u;
+}
+
+// ----------------------------------------------------------- small ops ----
+
+__global__ void fill_zero_kernel(float *y, size_t n) {
+  size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
+  if (i < n) y[i] = 0.f;
+}
+
+__global__ void add_bias_kernel(float *y, const uint16_t *b, size_t n) {
+  size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
+  if (i < n) y[i] = y[i] + bf16f(b[i]);
+}
+
+__global__ void embed_gather_kernel(float *out, const uint16_t *table, size_t hidden,
+                                    const uint32_t *token_dev, uint32_t token_host) {
+  const uint32_t tok = token_dev ? *token_dev : token_host;
+  const uint16_t *row = table + (size_t)tok * hidden;
+  for (size_t j = blockIdx.x * (size_t)blockDim.x + threadIdx.x; j < hidden;
+       j += (size_t)gridDim.x * blockDim.x)
+    out[j] = bf16f(row[j]);
+}
+
+__global__ void __launch_bounds__(kBlock)
+    rmsnorm_kernel(float *y, const uint16_t *g, const float *x, size_t n, float eps) {
+  __shared__ float red4[4];
+  float ss = 0.f;
+  for (size_t j = threadIdx.x; j < n; j += kBlock) ss += x[j] * x[j];
+  const float tot = block_sum(ss, red4);
+  const float inv = 1.0f / sqrtf(tot / (float)n + eps);
+  for (size_t j = threadIdx.x; j < n; j += kBlock) y[j] = bf16f(g[j]) * (x[j] * inv);
+}
+
+// cs[p] = (cos, sin) of pair p, evaluated on the host (rope.rs:186-193)
+__global__ void rope_apply_kernel(float *x, size_t len, size_t head_dim, const float2 *cs) {
+  const size_t half = head_dim / 2, pairs = len / 2;
+  size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
+  if (i >= pairs) return;
+  const size_t head = i / half, p = i - head * half;
+  const size_t i0 = head * head_dim + p, i1 = i0 + half;
+  const float x0 = x[i0], x1 = x[i1];
+  const float2 c = cs[p];
+  x[i0] = x0 * c.x - x1 * c.y;
+  x[i1] = x1 * c.x + x0 * c.y;
+}
+
+// Op-tier gqa_attn_f32 for any shape: one workgroup per query head; scores
+// in a global scratch row of length seq; the last head's probabilities are
+// also written to `probs` (gqa.rs:26-30).
+__global__ void __launch_bounds__(kBlock)
+    gqa_general_kernel(float *y, const float *q, const float *k, const float *v, float *probs,
+                       float *scr, int nq, int nkv, int d, int seq, int mask,
+                       unsigned long long qpos) {
+  __shared__ float red4[4];
+  const int h = blockIdx.x, g = h / (nq / nkv), tid = threadIdx.x;
+  const float scale = 1.0f / sqrtf((float)d);
+  float *s = scr + (size_t)h * seq;
+  const float *qh = q + (size_t)h * d;
+  auto kept = [&](int t) { return mask == 0 || (unsigned long long)t <= qpos; };
+  float mx = -INFINITY;
+  for (int t = tid; t < seq; t += kBlock) {
+    if (!kept(t)) continue;
+    const float *kt = k + ((size_t)g * seq + t) * d;
+    float acc = 0.f;
+    for (int j = 0; j < d; j++) acc = fmaf(qh[j], kt[j], acc);
+    s[t] = acc * scale;
+    mx = fmaxf(mx, s[t]);
+  }
+  // block max
+  mx = group_max<kWave>(mx);
+  __syncthreads();
+  if ((tid & 63) == 0) red4[tid >> 6] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(red4[0], red4[1]), fmaxf(red4[2], red4[3]));
+  float sum = 0.f;
+  for (int t = tid; t < seq; t += kBlock) {
+    if (!kept(t)) continue;
+    const float e = expf(s[t] - mx);
+    s[t] = e;
+    sum += e;
+  }
+  sum = block_sum(sum, red4);
+  for (int t = tid; t < seq; t += kBlock) {
+    const float p = kept(t) ? s[t] / sum : 0.f;
+    s[t] = p;
+    if (h == nq - 1) probs[t] = p;
+  }
+  __syncthreads();
+  for (int j = tid; j < d; j += kBlock) {
+    float acc = 0.f;
+    for (int t = 0; t < seq; t++)
+      if (kept(t)) acc = fmaf(s[t], v[((size_t)g * seq + t) * d + j], acc);
+    y[(size_t)h * d + j] = acc;
+  }
+}
+
+__global__ void swiglu_mul_kernel(float *h, const float *g, const float *u, size_t n) {
+  size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
+  if (i < n) h[i] = silu(g[i]) * u[i];
+}
+
+constexpr int kArgmaxPerBlock = 4096;
+
+__device__ float2 block_best(float bv, uint32_t bi, float2 *sh) {
+  // wave reduce then waves 0..3 in order
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float ov = __shfl_xor(bv, o, kWave);
+    const uint32_t oi = __shfl_xor(bi, o, kWave);
+    if (beats(ov, oi, bv, bi)) {
+      bv = ov;
+      bi = oi;
+    }
+  }
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane == 0) sh[wave] = make_float2(bv, __uint_as_float(bi));
+  __syncthreads();
+  float2 b = sh[0];
+  for (int t = 1; t < (int)(blockDim.x >> 6); t++)
+    if (beats(sh[t].x, __float_as_uint(sh[t].y), b.x, __float_as_uint(b.y))) b = sh[t];
+  return b;
+}
+
+__global__ void __launch_bounds__(kBlock)
+    argmax_partial_kernel(const float *logits, size_t n, float2 *part) {
+  __shared__ float2 sh[4];
+  float bv = -INFINITY;
+  uint32_t bi = 0xffffffffu;
+  const size_t base = (size_t)blockIdx.x * kArgmaxPerBlock;
+  for (size_t i = base + threadIdx.x; i < min(n, base + kArgmaxPerBlock); i += kBlock)
+    if (beats(logits[i], (uint32_t)i, bv, bi)) {
+      bv = logits[i];
+      bi = (uint32_t)i;
+    }
+  float2 b = block_best(bv, bi, sh);
+  if (threadIdx.x == 0) part[blockIdx.x] = b;
+}
+
+__global__ void __launch_bounds__(1024) argmax_final_kernel(ArgmaxFinalArgs a) {
+  __shared__ float2 sh[16];
+  __shared__ uint32_t tok_s;
+  float bv = -INFINITY;
+  uint32_t bi = 0xffffffffu;
+  const bool forced = a.state && a.state[3] == 1u;
+  if (!forced) {
+    for (int i = threadIdx.x; i < a.nparts; i += blockDim.x) {
+      const float2 p = a.part[i];
+      if (beats(p.x, __float_as_uint(p.y), bv, bi)) {
+        bv = p.x;
+        bi = __float_as_uint(p.y);
+      }
+    }
+    float2 b = block_best(bv, bi, sh);
+    if (threadIdx.x == 0) {
+      uint32_t idx = __float_as_uint(b.y);
+      tok_s = idx == 0xffffffffu ? 0u : idx;
+    }
+  } else if (threadIdx.x == 0) {
+    tok_s = a.state[1];
+  }
+  __syncthreads();
+  const uint32_t tok = tok_s;
+  if (threadIdx.x == 0) {
+    if (a.token_out) *a.token_out = tok;
+    if (a.state) {
+      a.state[1] = tok;
+      if (a.out_ids) a.out_ids[a.state[2]] = tok;
+      a.state[2] += 1u;
+    }
+  }
+  if (a.embed)
+    for (int j = threadIdx.x; j < a.hidden; j += blockDim.x)
+      a.x[j] = bf16f(a.embed[(size_t)tok * a.hidden + j]);
+}
+
+// ------------------------------------------------------------- prefill ----
+
+__global__ void embed_rows_kernel(float *X, const uint16_t *embed, const uint32_t *tokens,
+                                  int H) {
+  const int r = blockIdx.x;
+  const uint16_t *src = embed + (size_t)tokens[r] * H;
+  for (int j = threadIdx.x; j < H; j += blockDim.x) X[(size_t)r * H + j] = bf16f(src[j]);
+}
+
+__device__ __forceinline__ void split2(float x, uint16_t *hi, uint16_t *lo) {
+  const uint16_t h = f2bf(x);
+  *hi = h;
+  *lo = f2bf(x - bf16f(h));
+}
+
+__global__ void __launch_bounds__(kBlock)
+    rmsnorm_rows_split_kernel(const float *X, const uint16_t *g, float eps, int H, uint16_t *hi,
+                              uint16_t *lo) {
+  __shared__ float red4[4];
+  const size_t r = blockIdx.x;
+  const float *x = X + r * H;
+  float ss = 0.f;
+  for (int j = threadIdx.x; j < H; j += kBlock) ss += x[j] * x[j];
+  const float tot = block_sum(ss, red4);
+  const float inv = 1.0f / sqrtf(tot / (float)H + eps);
+  for (int j = threadIdx.x; j < H; j += kBlock)
+    split2(bf16f(g[j]) * (x[j] * inv), hi + r * H + j, lo + r * H + j);
+}
+
+__global__ void split_kernel(const float *X, size_t n, uint16_t *hi, uint16_t *lo) {
+  size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
+  if (i < n) split2(X[i], hi + i, lo + i);
+}
+
+// MFMA GEMM, C[M,N] = (A_hi + A_lo)[M,K] . W[N,K]^T, both operands K-contiguous.
+// Workgroup tile 128 (M) x 64 (N) x 64 (K); wave w owns rows 32w..32w+31 and
+// both 32-column halves: 2 accumulators of v_mfma_f32_32x32x16_bf16, each fed
+// by the hi and the lo term of A. Operand fragments: lane l holds row/col
+// (l % 32) and K-octet (l / 32) of a 16-wide K step, so A and W share the K
+// mapping; the 32x32 result sits at row 8*(i/4) + 4*(l/32) + i%4, col l%32.
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int GBM = 128, GBN = 64, GBK = 64, GLD = GBK + 8;  // LDS row pitch (bf16)
+
+__device__ __forceinline__ u32x4 load_tile8(const uint16_t *src, int row, int rows, int kk,
+                                            int K, bool vec) {
+  u32x4 v = {0u, 0u, 0u, 0u};
+  if (row >= rows) return v;
+  const uint16_t *p = src + (size_t)row * K + kk;
+  if (vec && kk + 8 <= K) return *(const u32x4 *)p;
+  uint16_t t[8];
+#pragma unroll
+  for (int e = 0; e < 8; e++) t[e] = kk + e < K ? p[e] : (uint16_t)0;
+  v[0] = t[0] | ((uint32_t)t[1] << 16);
+  v[1] = t[2] | ((uint32_t)t[3] << 16);
+  v[2] = t[4] | ((uint32_t)t[5] << 16);
+  v[3] = t[6] | ((uint32_t)t[7] << 16);
+  return v;
+}
+
+template <int EPI>
+__global__ void __launch_bounds__(kBlock) gemm_mfma_kernel(GemmArgs a) {
+  __shared__ __attribute__((aligned(16))) uint16_t ahi_s[GBM * GLD];
+  __shared__ __attribute__((aligned(16))) uint16_t alo_s[GBM * GLD];
+  __shared__ __attribute__((aligned(16))) uint16_t w_s[GBN * GLD];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int n0 = blockIdx.x * GBN, m0 = blockIdx.y * GBM;
+  const int M = a.M, N = a.N, K = a.K;
+  const bool vec = (K & 7) == 0;
+  f32x16 acc0, acc1;
+#pragma unroll
+  for (int i = 0; i < 16; i++) {
+    acc0[i] = 0.f;
+    acc1[i] = 0.f;
+  }
+  for (int k0 = 0; k0 < K; k0 += GBK) {
+    // A tiles: 128 rows x 8 octets = 1024 vectors; W tile: 64 x 8 = 512
+#pragma unroll
+    for (int it = 0; it < 4; it++) {
+      const int v = tid + it * kBlock, r = v >> 3, o = v & 7;
+      *(u32x4 *)&ahi_s[r * GLD + o * 8] = load_tile8(a.a_hi, m0 + r, M, k0 + o * 8, K, vec);
+      *(u32x4 *)&alo_s[r * GLD + o * 8] = load_tile8(a.a_lo, m0 + r, M, k0 + o * 8, K, vec);
+    }
+#pragma unroll
+    for (int it = 0; it < 2; it++) {
+      const int v = tid + it * kBlock, r = v >> 3, o = v & 7;
+      *(u32x4 *)&w_s[r * GLD + o * 8] = load_tile8(a.w, n0 + r, N, k0 + o * 8, K, vec);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int ks = 0; ks < GBK; ks += 16) {
+      const int kk = ks + (lane >> 5) * 8;
+      const int ar = wave * 32 + (lane & 31);
+      const bf16x8 ah = __builtin_bit_cast(bf16x8, *(const u32x4 *)&ahi_s[ar * GLD + kk]);
+      const bf16x8 al = __builtin_bit_cast(bf16x8, *(const u32x4 *)&alo_s[ar * GLD + kk]);
+      const bf16x8 b0 = __builtin_bit_cast(bf16x8, *(const u32x4 *)&w_s[(lane & 31) * GLD + kk]);
+      const bf16x8 b1 =
+          __builtin_bit_cast(bf16x8, *(const u32x4 *)&w_s[(32 + (lane & 31)) * GLD + kk]);
+      acc0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, b0, acc0, 0, 0, 0);
+      acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, b1, acc1, 0, 0, 0);
+      acc0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, b0, acc0, 0, 0, 0);
+      acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, b1, acc1, 0, 0, 0);
+    }
+    __syncthreads();
+  }
+  const int d = a.head_dim, half = d >> 1;
+#pragma unroll
+  for (int nh = 0; nh < 2; nh++) {
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+      const float c = nh ? acc1[i] : acc0[i];
+      const int row = m0 + wave * 32 + (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3);
+      const int col = n0 + nh * 32 + (lane & 31);
+      const float partner = __shfl_xor(c, 1, kWave);  // column col ^ 1, same row
+      if (row >= M || col >= N) continue;
+      if (EPI == EPI_STORE) {
+        a.y[(size_t)row * N + col] = c;
+      } else if (EPI == EPI_RESID) {
+        a.y[(size_t)row * N + col] += c;
+      } else if (EPI == EPI_GU) {
+        if ((col & 1) == 0) {
+          const size_t o = (size_t)row * (N >> 1) + (col >> 1);
+          split2(silu(c) * partner, a.h_hi + o, a.h_lo + o);
+        }
+      } else if (EPI == EPI_QKV) {
+        if ((col & 1) == 0) {
+          const int pos = a.start_pos + row;
+          const float y0 = c + a.bias[col], y1 = partner + a.bias[col + 1];
+          if (col < a.q_dim + a.kv_dim) {
+            const bool is_q = col < a.q_dim;
+            const int rr = is_q ? col : col - a.q_dim;
+            const int u = rr >> 1, head = u / half, p = u - head * half;
+            const float2 cs = a.rope[(size_t)pos * half + p];
+            const float o0 = y0 * cs.x - y1 * cs.y;
+            const float o1 = y1 * cs.x + y0 * cs.y;
+            if (is_q) {
+              float *qrow = a.q_out + (size_t)row * a.q_dim;
+              qrow[head * d + p] = o0;
+              qrow[head * d + p + half] = o1;
+            } else {
+              const size_t base = ((size_t)head * a.max_seq + pos) * d;
+              store_kv(a.kc, base + p, o0, a.kv_bf16);
+              store_kv(a.kc, base + p + half, o1, a.kv_bf16);
+            }
+          } else {
+            const int rr = col - a.q_dim - a.kv_dim;
+            const int head = rr / d, j = rr - head * d;
+            const size_t base = ((size_t)head * a.max_seq + pos) * d + j;
+            store_kv(a.vc, base, y0, a.kv_bf16);
+            store_kv(a.vc, base + 1, y1, a.kv_bf16);
+          }
+        }
+      }
+    }
+  }
+}
+
+// Causal prefill attention: workgroup = (query head, 32 queries); 8 lanes per
+// query each own dims j, j+8, ...; keys stream through LDS in tiles of 32 with
+// an online softmax. Query i sits at position start + i and sees keys <= it
+// (GqaMask::Causal, gqa.rs:80-86).
+constexpr int kPqPerBlock = 32, kPkTile = 32, kPdPerLane = kMaxHeadDim / 8;
+
+__global__ void __launch_bounds__(kBlock) attn_prefill_kernel(AttnPrefillArgs a) {
+  extern __shared__ float psm[];
+  const int d = a.head_dim;
+  float *k_s = psm;                   // [tile][d]
+  float *v_s = psm + kPkTile * d;     // [tile][d]
+  const int h = blockIdx.x, g = h / (a.nq / a.nkv);
+  const int tid = threadIdx.x, qi = blockIdx.y * kPqPerBlock + (tid >> 3), j = tid & 7;
+  const bool active = qi < a.M;
+  const int qpos = a.start_pos + (active ? qi : a.M - 1);
+  const int last_pos = a.start_pos + min(a.M - 1, (int)(blockIdx.y + 1) * kPqPerBlock - 1);
+  const float scale = 1.0f / sqrtf((float)d);
+  const int qd = a.nq * d;
+  float q[kPdPerLane], o[kPdPerLane];
+#pragma unroll
+  for (int e = 0; e < kPdPerLane; e++) {
+    const int dd = j + e * 8;
+    q[e] = (active && dd < d) ? a.q[(size_t)qi * qd + h * d + dd] : 0.f;
+    o[e] = 0.f;
+  }
+  float mx = -INFINITY, l = 0.f;
+  for (int t0 = 0; t0 <= last_pos; t0 += kPkTile) {
+    const int nt = min(kPkTile, last_pos + 1 - t0);
+    __syncthreads();
+    const size_t kv0 = ((size_t)g * a.max_seq + t0) * d;
+    for (int i = tid; i < nt * d; i += kBlock) {
+      k_s[i] = load_kv(a.kc, kv0 + i, a.kv_bf16);
+      v_s[i] = load_kv(a.vc, kv0 + i, a.kv_bf16);
+    }
+    __syncthreads();
+    for (int t = 0; t < nt; t++) {
+      float s = 0.f;
+#pragma unroll
+      for (int e = 0; e < kPdPerLane; e++) {
+        const int dd = j + e * 8;
+        if (dd < d) s = fmaf(q[e], k_s[t * d + dd], s);
+      }
+      s = group_sum<8>(s) * scale;
+      if (t0 + t <= qpos) {
+        const float mnew = fmaxf(mx, s);
+        const float corr = expf(mx - mnew);
+        const float p = expf(s - mnew);
+        l = l * corr + p;
+#pragma unroll
+        for (int e = 0; e < kPdPerLane; e++) {
+          const int dd = j + e * 8;
+          if (dd < d) o[e] = fmaf(p, v_s[t * d + dd], o[e] * corr);
+        }
+        mx = mnew;
+      }
+    }
+  }
+  if (!active) return;
+#pragma unroll
+  for (int e = 0; e < kPdPerLane; e++) {
+    const int dd = j + e * 8;
+    if (dd < d) {
+      const size_t idx = (size_t)qi * qd + h * d + dd;
+      split2(o[e] / l, a.out_hi + idx, a.out_lo + idx);
+    }
+  }
+}
+
+__global__ void permute_rows_kernel(uint16_t *dst, const uint16_t *src, const int *perm,
+                                    int cols) {
+  const int r = blockIdx.x;
+  const uint16_t *s = src + (size_t)perm[r] * cols;
+  uint16_t *o = dst + (size_t)r * cols;
+  for (int j = threadIdx.x; j < cols; j += blockDim.x) o[j] = s[j];
+}
+
+inline unsigned nblk(size_t n, unsigned b) { return (unsigned)((n + b - 1) / b); }
+
+}  // namespace
+
+// ============================================================ launchers ====
+
+namespace {
+template <int TEAM, int ROWS, int CPT, int XM, int EPI>
+hipError_t go_gemv(const GemvArgs &a, hipStream_t s, int *nparts) {
+  const int rows_per_block = ROWS * (kBlock / TEAM);
+  const unsigned grid = nblk((size_t)a.m, rows_per_block);
+  if (nparts) *nparts = (int)grid;
+  hipLaunchKernelGGL((gemv_kernel<TEAM, ROWS, CPT, XM, EPI>), dim3(grid), dim3(kBlock),
+                     (size_t)a.k * sizeof(float), s, a);
+  return hipGetLastError();
+}
+
+template <int XM, int EPI>
+hipError_t go_gemv_generic(const GemvArgs &a, hipStream_t s, int *nparts) {
+  const unsigned grid = nblk((size_t)a.m, 8);
+  if (nparts) *nparts = (int)grid;
+  hipLaunchKernelGGL((gemv_generic_kernel<XM, EPI>), dim3(grid), dim3(kBlock),
+                     (size_t)((a.k + 3) & ~3) * sizeof(float), s, a);
+  return hipGetLastError();
+}
+
+// Variant choice: rows per team grow with m (more independent loads in flight
+// per lane); a wavefront team while one wave's chunks cover the row in <= 8
+// steps, else the whole workgroup splits the row (k up to 24576).
+template <int XM, int EPI>
+hipError_t pick_gemv(const GemvArgs &a, hipStream_t s, int *nparts) {
+  const int nch = a.k / 8;
+  const bool vec = (a.k % 8) == 0 && a.k >= 8 && ((uintptr_t)a.w % 16) == 0 &&
+                   ((uintptr_t)a.x % 16) == 0 && (XM == X_PLAIN || ((uintptr_t)a.gamma % 8) == 0);
+  if (!vec || a.k > 24576) return go_gemv_generic<XM, EPI>(a, s, nparts);
+  const bool big = a.m >= 16384;
+  if (nch <= 64 * 8) {
+    const int cpt = (nch + 63) / 64;
+#define WAVE_CASE(C)                                                                     \
+  case C:                                                                                \
+    return big ? go_gemv<64, 4, C, XM, EPI>(a, s, nparts) : go_gemv<64, 2, C, XM, EPI>(a, s, nparts);
+    switch (cpt) {
+      WAVE_CASE(1)
+      WAVE_CASE(2)
+      WAVE_CASE(3)
+      WAVE_CASE(4)
+      case 5:
+      WAVE_CASE(6)
+      case 7:
+      WAVE_CASE(8)
+      default:
+        break;
+    }
+#undef WAVE_CASE
+  }
+  const int cpt = (nch + 255) / 256;
+  if (cpt <= 3) return go_gemv<256, 2, 3, XM, EPI>(a, s, nparts);
+  if (cpt <= 5) return go_gemv<256, 2, 5, XM, EPI>(a, s, nparts);
+  if (cpt <= 8) return go_gemv<256, 2, 8, XM, EPI>(a, s, nparts);
+  if (cpt <= 10) return go_gemv<256, 2, 10, XM, EPI>(a, s, nparts);
+  return go_gemv<256, 2, 12, XM, EPI>(a, s, nparts);
+}
+}  // namespace
+
+hipError_t launch_gemv(const GemvArgs &a, GemvX xm, GemvEpi epi, hipStream_t s, int *nparts) {
+  if (a.m <= 0) return hipSuccess;
+  if (xm == X_PLAIN && epi == EPI_STORE) return pick_gemv<X_PLAIN, EPI_STORE>(a, s, nparts);
+  if (xm == X_PLAIN && epi == EPI_RESID) return pick_gemv<X_PLAIN, EPI_RESID>(a, s, nparts);
+  if (xm == X_NORM && epi == EPI_QKV) return pick_gemv<X_NORM, EPI_QKV>(a, s, nparts);
+  if (xm == X_NORM && epi == EPI_GU) return pick_gemv<X_NORM, EPI_GU>(a, s, nparts);
+  if (xm == X_NORM && epi == EPI_HEAD) return pick_gemv<X_NORM, EPI_HEAD>(a, s, nparts);
+  return hipErrorInvalidValue;
+}
+
+int gemv_head_parts(int m, int k) {
+  const int nch = k / 8;
+  if (k % 8 != 0 || k < 8 || k > 24576) return (int)nblk((size_t)m, 8);
+  const bool big = m >= 16384;
+  if (nch <= 64 * 8) return (int)nblk((size_t)m, big ? 16 : 8);
+  return (int)nblk((size_t)m, 2);
+}
+
+int attn_decode_chunks(int max_seq) { return (max_seq + kAttnChunk - 1) / kAttnChunk; }
+
+size_t attn_decode_part_floats(int nq, int max_seq, int head_dim) {
+  return (size_t)nq * attn_decode_chunks(max_seq) * ((size_t)head_dim + 2);
+}
+
+hipError_t launch_attn_decode(const AttnDecodeArgs &a, hipStream_t s) {
+  const int gq = a.nq / a.nkv, d = a.head_dim;
+  if (gq > kMaxQPerKv || d > kMaxHeadDim) return hipErrorInvalidValue;
+  const size_t smem =
+      sizeof(float) * ((size_t)gq * d + (size_t)kAttnChunk * (d + 1) + (size_t)kAttnChunk * d +
+                       (size_t)gq * kAttnChunk + 2 * gq);
+  dim3 grid(a.nkv, attn_decode_chunks(a.max_seq));
+  hipLaunchKernelGGL(attn_decode_kernel, grid, dim3(kBlock), smem, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_fill_zero(float *y, size_t n, hipStream_t s) {
+  if (!n) return hipSuccess;
+  hipLaunchKernelGGL(fill_zero_kernel, dim3(nblk(n, 256)), dim3(256), 0, s, y, n);
+  return hipGetLastError();
+}
+
+hipError_t launch_add_bias(float *y, const uint16_t *b, size_t n, hipStream_t s) {
+  if (!n) return hipSuccess;
+  hipLaunchKernelGGL(add_bias_kernel, dim3(nblk(n, 256)), dim3(256), 0, s, y, b, n);
+  return hipGetLastError();
+}
+
+hipError_t launch_embed_gather(float *out, const uint16_t *table, size_t hidden,
+                               const uint32_t *token_dev, uint32_t token_host, hipStream_t s) {
+  hipLaunchKernelGGL(embed_gather_kernel, dim3(nblk(hidden, 256) > 64 ? 64 : nblk(hidden, 256)),
+                     dim3(256), 0, s, out, table, hidden, token_dev, token_host);
+  return hipGetLastError();
+}
+
+hipError_t launch_rmsnorm(float *y, const uint16_t *g, const float *x, size_t n, float eps,
+                          hipStream_t s) {
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3(1), dim3(kBlock), 0, s, y, g, x, n, eps);
+  return hipGetLastError();
+}
+
+hipError_t launch_rope_apply(float *x, size_t len, size_t head_dim, const float2 *cs,
+                             hipStream_t s) {
+  hipLaunchKernelGGL(rope_apply_kernel, dim3(nblk(len / 2, 256)), dim3(256), 0, s, x, len,
+                     head_dim, cs);
+  return hipGetLastError();
+}
+
+hipError_t launch_gqa_general(float *y, const float *q, const float *k, const float *v,
+                              float *probs, float *scratch, int nq, int nkv, int d, int seq,
+                              int mask, size_t query_pos, hipStream_t s) {
+  hipLaunchKernelGGL(gqa_general_kernel, dim3(nq), dim3(kBlock), 0, s, y, q, k, v, probs,
+                     scratch, nq, nkv, d, seq, mask, (unsigned long long)query_pos);
+  return hipGetLastError();
+}
+
+hipError_t launch_swiglu_mul(float *h, const float *g, const float *u, size_t n, hipStream_t s) {
+  hipLaunchKernelGGL(swiglu_mul_kernel, dim3(nblk(n, 256)), dim3(256), 0, s, h, g, u, n);
+  return hipGetLastError();
+}
+
+int argmax_parts(size_t n) { return (int)nblk(n, kArgmaxPerBlock); }
+
+hipError_t launch_argmax_partial(const float *logits, size_t n, float2 *part, hipStream_t s) {
+  hipLaunchKernelGGL(argmax_partial_kernel, dim3(argmax_parts(n)), dim3(kBlock), 0, s, logits, n,
+                     part);
+  return hipGetLastError();
+}
+
+hipError_t launch_argmax_final(const ArgmaxFinalArgs &a, hipStream_t s) {
+  hipLaunchKernelGGL(argmax_final_kernel, dim3(1), dim3(1024), 0, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_embed_rows(float *X, const uint16_t *embed, const uint32_t *tokens, int M,
+                             int H, hipStream_t s) {
+  hipLaunchKernelGGL(embed_rows_kernel, dim3(M), dim3(256), 0, s, X, embed, tokens, H);
+  return hipGetLastError();
+}
+
+hipError_t launch_rmsnorm_rows_split(const float *X, const uint16_t *g, float eps, int M, int H,
+                                     uint16_t *hi, uint16_t *lo, hipStream_t s) {
+  hipLaunchKernelGGL(rmsnorm_rows_split_kernel, dim3(M), dim3(kBlock), 0, s, X, g, eps, H, hi,
+                     lo);
+  return hipGetLastError();
+}
+
+hipError_t launch_split_rows(const float *X, size_t n, uint16_t *hi, uint16_t *lo,
+                             hipStream_t s) {
+  if (!n) return hipSuccess;
+  hipLaunchKernelGGL(split_kernel, dim3(nblk(n, 256)), dim3(256), 0, s, X, n, hi, lo);
+  return hipGetLastError();
+}
+
+hipError_t launch_gemm(const GemmArgs &a, GemvEpi epi, hipStream_t s) {
+  if (a.M <= 0 || a.N <= 0) return hipSuccess;
+  dim3 grid(nblk((size_t)a.N, GBN), nblk((size_t)a.M, GBM));
+  switch (epi) {
+    case EPI_STORE:
+      hipLaunchKernelGGL(gemm_mfma_kernel<EPI_STORE>, grid, dim3(kBlock), 0, s, a);
+      break;
+    case EPI_RESID:
+      hipLaunchKernelGGL(gemm_mfma_kernel<EPI_RESID>, grid, dim3(kBlock), 0, s, a);
+      break;
+    case EPI_GU:
+      hipLaunchKernelGGL(gemm_mfma_kernel<EPI_GU>, grid, dim3(kBlock), 0, s, a);
+      break;
+    case EPI_QKV:
+      hipLaunchKernelGGL(gemm_mfma_kernel<EPI_QKV>, grid, dim3(kBlock), 0, s, a);
+      break;
+    default:
+      return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_attn_prefill(const AttnPrefillArgs &a, hipStream_t s) {
+  if (a.head_dim > kMaxHeadDim) return hipErrorInvalidValue;
+  dim3 grid(a.nq, nblk((size_t)a.M, kPqPerBlock));
+  const size_t smem = sizeof(float) * 2 * kPkTile * a.head_dim;
+  hipLaunchKernelGGL(attn_prefill_kernel, grid, dim3(kBlock), smem, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_permute_rows(uint16_t *dst, const uint16_t *src, const int *perm, int rows,
+                               int cols, hipStream_t s) {
+  if (rows <= 0) return hipSuccess;
+  hipLaunchKernelGGL(permute_rows_kernel, dim3(rows), dim3(256), 0, s, dst, src, perm, cols);
+  return hipGetLastError();
+}
+
+const char *kernel_build_info() {
+  return "gfx950; gemv: wave/workgroup teams, 16B nontemporal bf16 loads, fused "
+         "rmsnorm/bias+rope+kv/swiglu/residual/argmax epilogues; attention: split-K "
+         "decode with last-block merge; prefill: v_mfma_f32_32x32x16_bf16 hi/lo GEMM";
+}
+
+}  // namespace myos

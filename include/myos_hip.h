@@ -1,0 +1,203 @@
+/*
+ * myos_hip.h -- C ABI of the MI355X (gfx950) implementation of the reference's
+ * batch-1 BF16-weight / FP32-accumulate token loop.
+ *
+ * Two tiers, both plain C: pointers + sizes + int status codes, no C++ or torch
+ * types. A caller that binds the reference's Rust API (a cgo/ctypes/Rust
+ * `extern "C"` block) maps one function to one reference function:
+ *
+ *  - op tier: the `tensor_core` re-exports (crates/tensor_core/src/lib.rs:54-74),
+ *    on DEVICE pointers, asynchronous on the given HIP stream (NULL = default
+ *    stream). Every slice argument of the reference (`&[u8]`, `&[f32]`) is a
+ *    (pointer, element count) pair here, and the reference's length checks
+ *    run on the host before anything is launched, so on a non-zero return no
+ *    output has been written ("on Err, outputs unchanged", bf16.rs:36-38).
+ *  - model tier: `model_core` (crates/model_core/src/lib.rs:21-26): KvCache +
+ *    BlockWorkspace + prefill / forward_token / greedy_decode over weights read
+ *    once from a BF16 SafeTensors file (qwen25_layout keys) into HBM. On a
+ *    non-zero return the KV cursor has not moved (qwen25_block.rs:129-135).
+ */
+#ifndef MYOS_HIP_H
+#define MYOS_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes: one per variant of the reference's error enums ---- */
+enum {
+  MYOS_OK = 0,
+  MYOS_E_SHAPE = 1,        /* Bf16OpError::Shape, GqaError/RopeError/SwigluError::Shape,
+                              BlockError::Shape, KvError::Shape */
+  MYOS_E_TOKEN = 2,        /* Bf16OpError::TokenOutOfBounds, BlockError::Token */
+  MYOS_E_ROW_OOB = 3,      /* Bf16OpError::RowOutOfBounds */
+  MYOS_E_POSITION = 4,     /* BlockError::Position, AttnError::Position */
+  MYOS_E_KV_FULL = 5,      /* KvError::Full */
+  MYOS_E_KV_RANGE = 6,     /* KvError::Range */
+  MYOS_E_W_MISSING = 7,    /* QwenBf16Error::Missing (weight_loader WeightError::NotFound) */
+  MYOS_E_W_DTYPE = 8,      /* QwenBf16Error::DType */
+  MYOS_E_W_SHAPE = 9,      /* QwenBf16Error::Shape */
+  MYOS_E_W_LENGTH = 10,    /* QwenBf16Error::Length / WeightError::LengthMismatch */
+  MYOS_E_IO = 11,          /* WeightFileError::Io */
+  MYOS_E_PARSE = 12,       /* WeightError::Parse / Duplicate / EmptyName / UnsupportedDType */
+  MYOS_E_HIP = 13,         /* a HIP runtime call failed (no reference counterpart) */
+  MYOS_E_ARG = 14,         /* NULL handle or pointer, unknown enum value */
+};
+
+typedef void *myos_stream_t; /* a hipStream_t */
+
+/* Text for a status code (static storage). */
+const char *myos_strerror(int status);
+/* Build identification: target arch and kernel variant names. */
+const char *myos_build_info(void);
+
+/* ======================= op tier (tensor_core) ======================= */
+
+/* gemv_bf16, crates/tensor_core/src/bf16.rs:80-122.
+ * y[m] = W[m,k] x[k]; W row-major little-endian BF16 with w_len ELEMENTS
+ * (the reference's byte length / 2; an odd byte count is not representable
+ * here). Checks in the reference's order: y_len != m or x_len != k -> SHAPE;
+ * k == 0: w_len != 0 -> SHAPE, else y = 0; w_len / k < m -> ROW_OOB;
+ * w_len != m*k -> SHAPE. f32 accumulate (the per-row sum order differs from
+ * the reference's serial chain; see the parity tolerance of the tests). */
+int myos_gemv_bf16(float *y, size_t y_len, const uint16_t *w, size_t w_len, const float *x,
+                   size_t x_len, size_t m, size_t k, myos_stream_t stream);
+
+/* gemm_bf16, crates/tensor_core/src/gemm_bf16.rs:51-110 (prefill projection).
+ * Y[batch,m] = X[batch,k] W[m,k]^T on MFMA (v_mfma_f32_32x32x16_bf16) with X
+ * split into two BF16 terms (hi + lo) so the f32 activations keep ~16 mantissa
+ * bits. The reference's caller-provided scratch is internal here. */
+int myos_gemm_bf16(float *y, size_t y_len, const uint16_t *w, size_t w_len, const float *x,
+                   size_t x_len, size_t batch, size_t m, size_t k, myos_stream_t stream);
+
+/* add_bf16_bias, bf16.rs:147-158: y[i] += bf16(bias[i]); bias_len != y_len -> SHAPE. */
+int myos_add_bf16_bias(float *y, size_t y_len, const uint16_t *bias, size_t bias_len,
+                       myos_stream_t stream);
+
+/* embed_gather_bf16, bf16.rs:165-198: out[hidden] = table[token, :].
+ * shape = [vocab, hidden]; out_len != hidden -> SHAPE; token >= vocab -> TOKEN;
+ * row past table_len -> ROW_OOB; table_len != vocab*hidden -> SHAPE. */
+int myos_embed_gather_bf16(float *out, size_t out_len, const uint16_t *table, size_t table_len,
+                           size_t vocab, size_t hidden, uint32_t token, myos_stream_t stream);
+
+/* rmsnorm_bf16_weight, bf16.rs:231-270: y = g * (x * 1/sqrtf(mean(x^2) + eps)).
+ * n == 0 or length mismatch -> SHAPE. */
+int myos_rmsnorm_bf16_weight(float *y, size_t y_len, const uint16_t *weight, size_t weight_len,
+                             const float *x, size_t x_len, float eps, myos_stream_t stream);
+
+/* rope_f32_inplace, crates/tensor_core/src/rope.rs:119-184 (NeoX half-rotate).
+ * The per-pair angles are evaluated on the host exactly as the reference does
+ * (f32 pos * 1/powf(theta, 2i/d), cosf/sinf) and applied on the device.
+ * head_dim zero/odd, len zero or not a multiple of head_dim -> SHAPE. */
+int myos_rope_f32_inplace(float *x, size_t len, uint32_t position, size_t head_dim, float theta,
+                          myos_stream_t stream);
+
+/* gqa_attn_f32, crates/tensor_core/src/gqa.rs:174-218. mask: 0 = Full,
+ * 1 = Causal{query_pos}. q,y: [nq, d]; k,v: [nkv, seq, d]; probs: [seq]
+ * (scratch; written with the last head's probabilities like the reference).
+ * Shape rules of gqa.rs:231-264 -> SHAPE. */
+int myos_gqa_attn_f32(float *y, size_t y_len, const float *q, size_t q_len, const float *k,
+                      size_t k_len, const float *v, size_t v_len, float *probs,
+                      size_t probs_len, size_t num_q_heads, size_t num_kv_heads,
+                      size_t head_dim, size_t seq_len, int mask, size_t query_pos,
+                      myos_stream_t stream);
+
+/* swiglu_mul_f32, crates/tensor_core/src/swiglu.rs:125-131: h = silu(g) * u. */
+int myos_swiglu_mul_f32(float *h, size_t h_len, const float *gate, size_t gate_len,
+                        const float *up, size_t up_len, myos_stream_t stream);
+
+/* greedy_token, crates/model_core/src/lib.rs:157-167: first index of the
+ * strict maximum (ties -> lowest index, NaN never wins, all -inf/NaN -> 0).
+ * Two-pass block argmax; the u32 result is written to DEVICE memory *out. */
+int myos_greedy_token(uint32_t *out, const float *logits, size_t n, myos_stream_t stream);
+
+/* Block until the stream's work is done; returns MYOS_E_HIP on a device error. */
+int myos_stream_sync(myos_stream_t stream);
+
+/* ======================= model tier (model_core) ===================== */
+
+typedef struct myos_model myos_model;
+
+/* BlockShape (qwen25_block.rs:53-75) + AttnShape (attn_wire.rs:44-63). */
+typedef struct {
+  size_t hidden, num_q_heads, num_kv_heads, head_dim, intermediate, vocab, num_layers;
+  float rms_eps, rope_theta;
+  int tied_head; /* 1: logits = embed_tokens (the reference); 0: lm_head.weight */
+} myos_block_shape;
+
+/* BlockShape::qwen25_1_5b (qwen25_block.rs:66-74) and the 7B analogue
+ * (hidden 3584, intermediate 18944, 28/4 heads, vocab 152064, untied head). */
+enum { MYOS_SHAPE_QWEN25_1_5B = 0, MYOS_SHAPE_QWEN25_7B = 1 };
+int myos_block_shape_preset(int preset, myos_block_shape *out);
+
+enum { MYOS_KV_F32 = 0, MYOS_KV_BF16 = 1 };
+
+/* Open: map `path` (SafeTensors), check every tensor the shape needs
+ * (preflight_weights, qwen25_block.rs:599-643), upload them once to HBM
+ * through pinned staging, allocate the KV cache [layers][kv][max_seq][d]
+ * (KvCache::new, kv_cache.rs:99-125) and the workspace (BlockWorkspace::new,
+ * qwen25_block.rs:97-114). Errors: IO / PARSE / W_* / SHAPE / HIP. */
+int myos_model_open(const char *path, const myos_block_shape *shape, int kv_dtype,
+                    size_t max_seq, myos_model **out);
+void myos_model_close(myos_model *m);
+
+/* prefill, qwen25_block.rs:323-543: the prompt as one chunk (MFMA GEMMs),
+ * causal attention, logits for the last id, cursor += n. */
+int myos_prefill(myos_model *m, const uint32_t *tokens, size_t n);
+/* forward_token, qwen25_block.rs:220-304. pos must equal the cursor. */
+int myos_forward_token(myos_model *m, uint32_t token, size_t pos);
+/* greedy_decode, qwen25_block.rs:765-780: token = argmax(logits), forward,
+ * append; `out` receives `steps` ids (host memory). A KV-full stop returns
+ * MYOS_E_KV_FULL after the steps that fit, like the reference's loop. Each
+ * step is one hipGraph replay when graphs are enabled (the default). */
+int myos_greedy_decode(myos_model *m, size_t steps, uint32_t *out);
+
+size_t myos_cache_len(const myos_model *m);        /* KvCache::len */
+/* KvCache::clear (kv_cache.rs:234-237): cursor back to 0, slots kept. */
+int myos_cache_clear(myos_model *m);
+size_t myos_max_seq(const myos_model *m);
+/* Host copies of the last forward's outputs: logits[vocab] (BlockWorkspace::logits),
+ * hidden[hidden] = residual stream after the last layer, normed[hidden] = final
+ * RMSNorm output (the head's input). */
+int myos_copy_logits(const myos_model *m, float *out, size_t n);
+int myos_copy_hidden(const myos_model *m, float *out, size_t n);
+int myos_copy_normed(const myos_model *m, float *out, size_t n);
+/* KvCache::key_head / value_head (kv_cache.rs:240-252) as f32 host copies. */
+int myos_kv_read(const myos_model *m, size_t layer, size_t head, size_t pos, float *k, float *v);
+/* 1 = capture each decode step in a hipGraph (default), 0 = plain launches. */
+int myos_set_graph(myos_model *m, int enabled);
+/* Device time of the last prefill / greedy_decode (hipEvent, milliseconds). */
+double myos_last_prefill_ms(const myos_model *m);
+double myos_last_decode_ms(const myos_model *m);
+/* Device bytes held by weights / KV cache / workspace. */
+size_t myos_weight_bytes(const myos_model *m);
+size_t myos_kv_bytes(const myos_model *m);
+
+/* Measurement hook (no reference counterpart): average device time of one
+ * decode-step kernel class, from a hipGraph holding that kernel once per
+ * layer (distinct weights, so no cache reuse across launches), replayed
+ * `reps` times between two hipEvents on the model's stream. Clobbers the
+ * decode activations (x, q, h) and the cache slot at the cursor: call it
+ * after the decode being measured. which: MYOS_K_* below. */
+enum { MYOS_K_QKV = 0, MYOS_K_ATTN = 1, MYOS_K_O = 2, MYOS_K_GATE_UP = 3, MYOS_K_DOWN = 4,
+       MYOS_K_HEAD = 5 };
+int myos_time_kernel(myos_model *m, int which, int reps, double *avg_ms);
+/* Algorithmic HBM bytes one launch of that kernel class moves at the current
+ * cursor (weights + biases + norm gains + KV read/written + activations). */
+double myos_kernel_bytes(const myos_model *m, int which);
+
+/* Seeded random-init writer for the benchmark models (no reference
+ * counterpart; the reference reads real checkpoints): every matrix and bias
+ * ~ N(0, std) rounded to BF16 (RNE), norm gains 1.0, qwen25_layout keys
+ * (+ lm_head.weight when untied). Generator: per tensor a SplitMix64 counter
+ * stream seeded with seed ^ FNV-1a64(name), Box-Muller in double. */
+int myos_write_random_qwen25(const char *path, const myos_block_shape *shape, uint64_t seed,
+                             float std_dev, int threads);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

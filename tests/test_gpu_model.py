@@ -1,0 +1,206 @@
+"""Model-tier parity on the GPU against the oracle (model_core restated).
+
+* the reference's block fixture: logits [1, 2, 0, -1], greedy ids [1, 1, 1, 1]
+  (qwen25_block.rs:1011-1071, 1200-1221) -- exact in any summation order;
+* the chunk-prefill fixture (rich_map, qwen25_block.rs:1423-1478): the GPU's
+  MFMA prefill and its GEMV forward_token both agree with the oracle;
+* seeded random small models, f32 and bf16 KV;
+* the Qwen2.5-1.5B shape: prompt [0] + 4 greedy steps, and 128 prompt ids +
+  teacher-forced decode, under the tolerance rule in parity.py.
+"""
+import importlib
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+from model_fixtures import (block_fixture, random_map, rich_map, rich_shape, shape_dict,
+                            write_safetensors)
+from parity import assert_logits_parity, max_rel, top2_gap
+
+myos = importlib.import_module("an-operating-system-for-ai-models-and-tensor-inference_amd")
+pytestmark = pytest.mark.gpu
+
+
+def to_block_shape(s, tied=True):
+    return myos.make_shape(s["hidden"], s["num_q_heads"], s["num_kv_heads"], s["head_dim"],
+                           s["intermediate"], s["vocab"], s["num_layers"],
+                           rms_eps=float(s["rms_eps"]), rope_theta=float(s["rope_theta"]),
+                           tied_head=tied)
+
+
+def open_pair(tmp_path, s, t, max_seq, kv=myos.KV_F32, name="m.safetensors", tied=True):
+    path = str(tmp_path / name)
+    write_safetensors(path, t)
+    g = myos.Model.open(path, to_block_shape(s, tied), kv, max_seq)
+    o = oracle.Model(s, t, max_seq, threads=4)
+    return g, o
+
+
+def test_block_fixture(tmp_path):
+    s, t = block_fixture()
+    g, o = open_pair(tmp_path, s, t, 8)
+    g.forward_token(0, 0)
+    assert list(g.logits()) == [1.0, 2.0, 0.0, -1.0]
+    assert g.cache_len() == 1
+    k, v = g.kv(0, 0, 0)
+    assert list(k) == [0.0, 0.0] and list(v) == [1.0, 0.0]
+    assert list(g.greedy_decode(4)) == [1, 1, 1, 1]
+    assert g.cache_len() == 5
+    assert list(g.kv(0, 0, 4)[1]) == [1.0, 0.0]
+    # prefill path on a fresh model
+    g2 = myos.Model.open(str(tmp_path / "m.safetensors"), to_block_shape(s), myos.KV_F32, 8)
+    with pytest.raises(myos.MyosError) as e:
+        g2.prefill([])
+    assert e.value.kind == "Shape" and g2.cache_len() == 0
+    g2.prefill([0])
+    assert list(g2.logits()) == [1.0, 2.0, 0.0, -1.0]
+    assert g2.greedy_decode(4) == [1, 1, 1, 1] and g2.cache_len() == 5
+    for gm in (g, g2):
+        gm.close()
+
+
+def test_errors_do_not_advance(tmp_path):
+    # qwen25_block.rs:1224-1300, 1481-1513
+    s, t = block_fixture()
+    path = str(tmp_path / "f.safetensors")
+    write_safetensors(path, t)
+    g = myos.Model.open(path, to_block_shape(s), myos.KV_F32, 2)
+    for call, kind in ((lambda: g.forward_token(0, 1), "Position"),
+                       (lambda: g.forward_token(9, 0), "TokenOutOfBounds"),
+                       (lambda: g.prefill([0, 9]), "TokenOutOfBounds"),
+                       (lambda: g.prefill([0, 0, 0]), "Full")):
+        with pytest.raises(myos.MyosError) as e:
+            call()
+        assert e.value.kind == kind and g.cache_len() == 0
+    assert list(g.logits()) == [0.0] * 4
+    g.forward_token(0, 0)
+    g.forward_token(1, 1)
+    before = g.logits()
+    with pytest.raises(myos.MyosError) as e:
+        g.forward_token(1, 2)
+    assert e.value.kind == "Full" and g.cache_len() == 2
+    assert np.array_equal(g.logits(), before)
+    with pytest.raises(myos.MyosError) as e:
+        g.greedy_decode(3)
+    assert e.value.kind == "Full" and e.value.partial == []
+    g.close()
+
+
+def _kv_all(m, s, n):
+    out = []
+    for l in range(s["num_layers"]):
+        for h in range(s["num_kv_heads"]):
+            for p in range(n):
+                k, v = m.kv(l, h, p)
+                out.append(np.concatenate([k, v]))
+    return np.stack(out)
+
+
+@pytest.mark.parametrize("graph", [True, False])
+def test_rich_map_chunk_and_serial(tmp_path, graph):
+    s = rich_shape(2)
+    t = rich_map(s)
+    g, o = open_pair(tmp_path, s, t, 16)
+    g.set_graph(graph)
+    gs = myos.Model.open(str(tmp_path / "m.safetensors"), to_block_shape(s), myos.KV_F32, 16)
+    gs.set_graph(graph)
+    for m in (g, gs):
+        m.forward_token(2, 0)
+    assert o.forward_token(2, 0) == 0
+    prompt = [1, 3, 0, 4, 2]
+    g.prefill(prompt)                      # chunk (MFMA)
+    for i, tok in enumerate(prompt):       # serial (GEMV)
+        gs.forward_token(tok, 1 + i)
+    assert o.prefill(prompt) == 0
+    ref = o.logits()
+    for m in (g, gs):
+        assert_logits_parity(m.logits(), ref, "rich_map")
+        assert max_rel(m.hidden(), o.hidden()) < 1e-4
+        assert max_rel(_kv_all(m, s, 6), _kv_all(o, s, 6)) < 1e-4
+    rc, ids = o.greedy_decode(3)
+    assert g.greedy_decode(3) == list(ids) == gs.greedy_decode(3)
+    g.close()
+    gs.close()
+
+
+@pytest.mark.parametrize("kv", [myos.KV_F32, myos.KV_BF16])
+@pytest.mark.parametrize("dims", [(256, 4, 2, 64, 512, 1000, 3), (128, 6, 1, 32, 384, 777, 2),
+                                  (384, 12, 2, 32, 1000, 4099, 2)])
+def test_random_small_models(tmp_path, kv, dims):
+    s = shape_dict(*dims, 1e-6)
+    t = random_map(s, seed=sum(dims), std=0.05)
+    g, o = open_pair(tmp_path, s, t, 40, kv=kv)
+    rng = np.random.default_rng(7)
+    prompt = rng.integers(0, s["vocab"], 17)
+    g.prefill(prompt)
+    assert o.prefill(prompt) == 0
+    tol = 1e-4 if kv == myos.KV_F32 else 2e-2
+    assert max_rel(g.logits(), o.logits()) < tol
+    assert max_rel(g.hidden(), o.hidden()) < tol
+    # teacher-forced decode: both fed the oracle's greedy id
+    for step in range(12):
+        tok = oracle.greedy_token(o.logits())
+        pos = o.cache_len()
+        assert o.forward_token(tok, pos) == 0
+        g.forward_token(tok, pos)
+        assert max_rel(g.logits(), o.logits()) < tol, step
+        if kv == myos.KV_F32:
+            assert_logits_parity(g.logits(), o.logits(), f"step {step}")
+    g.close()
+
+
+# -------------------------------------------------- Qwen2.5-1.5B shape ----
+
+@pytest.fixture(scope="module")
+def qwen15(tmp_path_factory):
+    path = os.environ.get("MYOS_TEST_WEIGHTS_1_5B")
+    if not path:
+        path = str(tmp_path_factory.mktemp("w") / "qwen25_1_5b_seed0.safetensors")
+        myos.write_random_qwen25(path, myos.preset(myos.SHAPE_QWEN25_1_5B), seed=0, std=0.02)
+    s = shape_dict(1536, 12, 2, 128, 8960, 151936, 28, 1e-6)
+    return path, s, oracle.load_safetensors_bits(path)
+
+
+def test_qwen15_prompt0_four_steps(qwen15):
+    # prompt [0], 4 greedy steps, batch 1 (max_seq 5)
+    path, s, t = qwen15
+    g = myos.Model.open(path, myos.preset(myos.SHAPE_QWEN25_1_5B), myos.KV_F32, 5)
+    o = oracle.Model(s, t, 5, threads=16)
+    g.prefill([0])
+    assert o.prefill([0]) == 0
+    assert_logits_parity(g.logits(), o.logits(), "prefill [0]")
+    assert max_rel(g.hidden(), o.hidden()) < 1e-2
+    ids_g = g.greedy_decode(4)
+    rc, ids_o = o.greedy_decode(4)
+    assert rc == 0
+    assert ids_g == [int(v) for v in ids_o]
+    assert_logits_parity(g.logits(), o.logits(), "after 4 steps")
+    assert max_rel(g.hidden(), o.hidden()) < 1e-2
+    g.close()
+
+
+def test_qwen15_prefill128_teacher_forced(qwen15):
+    # 128 seeded prompt ids prefilled on MFMA, then teacher-forced steps
+    path, s, t = qwen15
+    rng = np.random.default_rng(2024)
+    prompt = rng.integers(0, 151936, 128)
+    g = myos.Model.open(path, myos.preset(myos.SHAPE_QWEN25_1_5B), myos.KV_F32, 256)
+    o = oracle.Model(s, t, 256, threads=16)
+    g.prefill(prompt)
+    assert o.prefill(prompt) == 0
+    errs = [assert_logits_parity(g.logits(), o.logits(), "prefill 128")]
+    assert max_rel(g.hidden(), o.hidden()) < 1e-2
+    for step in range(6):
+        tok = oracle.greedy_token(o.logits())
+        pos = o.cache_len()
+        assert o.forward_token(tok, pos) == 0
+        g.forward_token(tok, pos)
+        errs.append(assert_logits_parity(g.logits(), o.logits(), f"step {step}"))
+        assert max_rel(g.hidden(), o.hidden()) < 1e-2
+    k_g, v_g = g.kv(27, 1, 130)
+    k_o, v_o = o.kv(27, 1, 130)
+    assert max_rel(k_g, k_o) < 1e-2 and max_rel(v_g, v_o) < 1e-2
+    print("max logits rel err per step:", ["%.2e" % e for e in errs])
+    g.close()

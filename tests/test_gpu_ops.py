@@ -1,0 +1,203 @@
+"""Op-tier parity on the GPU: each C-ABI op against the oracle on seeded inputs.
+
+Shapes: the five GEMV shapes of the isolated-kernel microbench (lm_head
+151936x1536, gate/up 8960x1536, down 1536x8960, q/o 1536x1536, k/v 256x1536)
+plus tails that take the generic kernel (k % 8 != 0), and the reference's
+own hand cases.
+"""
+import importlib
+
+import numpy as np
+import pytest
+
+import oracle
+from model_fixtures import THETA, bits, rne_bf16
+from parity import dot_bound, max_rel
+
+torch = pytest.importorskip("torch")
+myos = importlib.import_module("an-operating-system-for-ai-models-and-tensor-inference_amd")
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+
+
+def dev(a, dtype=None):
+    t = torch.from_numpy(np.ascontiguousarray(a))
+    if dtype is not None:
+        t = t.view(dtype)
+    return t.to(DEV)
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def rand_w(rng, m, k):
+    return rne_bf16(rng.standard_normal((m, k), dtype=np.float32) * np.float32(0.02))
+
+
+MICRO = [(151936, 1536), (8960, 1536), (1536, 8960), (1536, 1536), (256, 1536)]
+
+
+@pytest.mark.parametrize("m,k", MICRO + [(17920, 1536), (2048, 1536), (3584, 18944),
+                                         (7, 3), (9, 17), (33, 24), (5, 1000), (40, 4104)])
+def test_gemv_vs_oracle(m, k):
+    rng = np.random.default_rng(m * 31 + k)
+    w = rand_w(rng, m, k)
+    x = rng.standard_normal(k, dtype=np.float32)
+    ref = oracle.gemv_bf16(w, x, m, k, threads=8)
+    y = torch.full((m,), 7.0, dtype=torch.float32, device=DEV)
+    myos.gemv_bf16(y, dev(w, torch.int16), dev(x), m, k)
+    got = host(y)
+    bound = dot_bound(oracle.bf16_to_f32(w), x)
+    assert np.all(np.abs(got.astype(np.float64) - ref) <= bound)
+    assert max_rel(got, ref) < 1e-5
+
+
+def test_gemv_hand_values_and_errors():
+    w = dev(bits([1.0, 2.0, 0.5, -1.0, 4.0, 1.5]), torch.int16)
+    x = dev(np.array([1.0, -2.0, 0.5], np.float32))
+    y = torch.zeros(2, dtype=torch.float32, device=DEV)
+    myos.gemv_bf16(y, w, x, 2, 3)
+    assert list(host(y)) == [-2.75, -8.25]
+    # k == 0 fills zero; errors leave y untouched
+    y = torch.tensor([1.0, 2.0], device=DEV)
+    myos.gemv_bf16(y, torch.zeros(0, dtype=torch.int16, device=DEV),
+                   torch.zeros(0, device=DEV), 2, 0)
+    assert list(host(y)) == [0.0, 0.0]
+    kept = torch.tensor([7.0, 8.0], device=DEV)
+    with pytest.raises(myos.MyosError) as e:
+        myos.gemv_bf16(kept, dev(bits([1.0, 2.0]), torch.int16), dev(np.ones(2, np.float32)), 2, 2)
+    assert e.value.kind == "RowOutOfBounds" and list(host(kept)) == [7.0, 8.0]
+
+
+def test_gemv_order_cancellation():
+    # gemv_bf16_kernel.rs:929-951: exact in any summation order only if the
+    # 2^24 terms cancel before the ones are absorbed; record what the GPU gives
+    row = [16777216.0, 1.0, 1.0, 1.0, -16777216.0, 1.0, 1.0, 1.0]
+    w = dev(bits(np.tile(row, 64)), torch.int16)
+    y = torch.zeros(64, device=DEV)
+    myos.gemv_bf16(y, w, dev(np.ones(8, np.float32)), 64, 8)
+    got = host(y)
+    # any order: the result is one of the values a reordering can produce
+    assert np.all(np.isin(got, [0.0, 1.0, 2.0, 3.0, 4.0]))
+
+
+@pytest.mark.parametrize("batch,m,k", [(128, 1536, 1536), (128, 256, 1536), (37, 8960, 1536),
+                                       (128, 1536, 8960), (5, 7, 3), (33, 70, 45),
+                                       (200, 130, 200)])
+def test_gemm_vs_oracle(batch, m, k):
+    rng = np.random.default_rng(batch + m + k)
+    w = rand_w(rng, m, k)
+    x = rng.standard_normal((batch, k), dtype=np.float32)
+    ref = oracle.gemm_bf16(w, x, batch, m, k, threads=8)
+    y = torch.zeros((batch, m), dtype=torch.float32, device=DEV)
+    myos.gemm_bf16(y, dev(w, torch.int16), dev(x), batch, m, k)
+    got = host(y)
+    # hi + lo split keeps x to within 2^-17 |x| (two RNE roundings of 2^-9)
+    # MFMA accumulation may not round to nearest: allow 4 gamma_k
+    bound = dot_bound(oracle.bf16_to_f32(w), x, extra_rel=2.0 ** -17, gamma_mult=4).T
+    assert np.all(np.abs(got.astype(np.float64) - ref) <= bound)
+
+
+def test_bias_embed_rmsnorm_swiglu():
+    rng = np.random.default_rng(3)
+    y0 = rng.standard_normal(1536).astype(np.float32)
+    b = rand_w(rng, 1, 1536)[0]
+    y = dev(y0)
+    myos.add_bf16_bias(y, dev(b, torch.int16))
+    assert np.array_equal(host(y), oracle.add_bf16_bias(y0, b))  # one f32 add: exact
+
+    table = rand_w(rng, 1000, 1536)
+    out = torch.zeros(1536, device=DEV)
+    myos.embed_gather_bf16(out, dev(table, torch.int16), (1000, 1536), 417)
+    assert np.array_equal(host(out), oracle.embed_gather_bf16(table, 1000, 1536, 417)[1])
+    with pytest.raises(myos.MyosError) as e:
+        myos.embed_gather_bf16(out, dev(table, torch.int16), (1000, 1536), 1000)
+    assert e.value.kind == "TokenOutOfBounds"
+
+    x = rng.standard_normal(1536).astype(np.float32)
+    g = rand_w(rng, 1, 1536)[0]
+    y = torch.zeros(1536, device=DEV)
+    myos.rmsnorm_bf16_weight(y, dev(g, torch.int16), dev(x), np.float32(1e-6))
+    assert max_rel(host(y), oracle.rmsnorm_bf16_weight(g, x, np.float32(1e-6))) < 1e-6
+    # hand values (bf16.rs:469-486) are exact in any order
+    y = torch.zeros(4, device=DEV)
+    myos.rmsnorm_bf16_weight(y, dev(bits([1.5, 4.0, -2.0, 0.5]), torch.int16),
+                             dev(np.array([8.0, 0, 0, 0], np.float32)), 0.0)
+    assert list(host(y)) == [3.0, 0.0, 0.0, 0.0]
+
+    gate = rng.standard_normal(8960).astype(np.float32) * 3
+    up = rng.standard_normal(8960).astype(np.float32)
+    h = torch.zeros(8960, device=DEV)
+    myos.swiglu_mul_f32(h, dev(gate), dev(up))
+    assert max_rel(host(h), oracle.swiglu_mul_f32(gate, up)) < 1e-6
+
+
+@pytest.mark.parametrize("pos,d,heads", [(1, 2, 1), (3, 4, 2), (8, 128, 12), (2303, 128, 2),
+                                         (0, 128, 12)])
+def test_rope(pos, d, heads):
+    rng = np.random.default_rng(pos + d)
+    x0 = rng.standard_normal(heads * d).astype(np.float32)
+    _, ref = oracle.rope_f32_inplace(x0, pos, d, THETA)
+    x = dev(x0)
+    myos.rope_f32_inplace(x, pos, d, THETA)
+    got = host(x)
+    # angles are the reference's (host libm); only the 2-term combine may
+    # round differently (a fused multiply-add), so within 2 ulp of |x0|+|x1|
+    assert np.all(np.abs(got - ref) <= 8 * 2.0 ** -24 * np.abs(x0).max())
+    if pos == 0:
+        assert np.array_equal(got, x0)
+
+
+def test_rope_hand_bits():
+    x = dev(np.array([1.0, 0.0], np.float32))
+    myos.rope_f32_inplace(x, 1, 2, THETA)
+    assert [int(v) for v in host(x).view(np.uint32)] == [0x3F0A5140, 0x3F576AA4]
+
+
+@pytest.mark.parametrize("nq,nkv,d,seq,causal", [(12, 2, 128, 1, None), (12, 2, 128, 256, None),
+                                                 (12, 2, 128, 300, 150), (4, 2, 1, 2, None),
+                                                 (28, 4, 128, 700, None), (1, 1, 4, 2, 0)])
+def test_gqa(nq, nkv, d, seq, causal):
+    rng = np.random.default_rng(nq * seq + d)
+    q = rng.standard_normal(nq * d).astype(np.float32)
+    k = rng.standard_normal(nkv * seq * d).astype(np.float32)
+    v = rng.standard_normal(nkv * seq * d).astype(np.float32)
+    ref, probs_ref = oracle.gqa_attn_f32(q, k, v, nq, nkv, d, seq, causal)
+    y = torch.zeros(nq * d, device=DEV)
+    probs = torch.zeros(seq, device=DEV)
+    myos.gqa_attn_f32(y, dev(q), dev(k), dev(v), probs, nq, nkv, d, seq, causal)
+    assert max_rel(host(y), ref) < 1e-5
+    assert max_rel(host(probs), probs_ref) < 1e-5
+
+
+def test_gqa_hand_bits_close():
+    # gqa.rs:366-401
+    y = torch.zeros(4, device=DEV)
+    probs = torch.zeros(2, device=DEV)
+    myos.gqa_attn_f32(y, dev(np.array([1, 1, 4, 4], np.float32)),
+                      dev(np.array([1, 0, 0, 2], np.float32)),
+                      dev(np.array([10, 0, 0, 7], np.float32)), probs, 4, 2, 1, 2)
+    ref = np.array([0x40E9F052, 0x40E9F052, 0x40DFECC5, 0x40DFECC5], np.uint32).view(np.float32)
+    assert max_rel(host(y), ref) < 1e-6
+
+
+@pytest.mark.parametrize("case", ["ties", "nan", "allnan", "neginf", "big"])
+def test_greedy_token(case):
+    rng = np.random.default_rng(11)
+    if case == "big":
+        lg = rng.standard_normal(151936).astype(np.float32)
+        lg[[5000, 140000]] = 9.0  # tie across blocks: lowest index wins
+    elif case == "ties":
+        lg = np.array([1.0, 3.0, 3.0, 2.0], np.float32)
+    elif case == "nan":
+        lg = np.array([np.nan, 1.0, np.nan], np.float32)
+    elif case == "allnan":
+        lg = np.full(9000, np.nan, np.float32)
+    else:
+        lg = np.full(5, -np.inf, np.float32)
+        lg[3] = np.nan
+    assert myos.greedy_token(dev(lg)) == oracle.greedy_token(lg)
