@@ -8,7 +8,9 @@
 namespace myos {
 
 // ---- GEMV family: one launch streams a row-major BF16 matrix once ----------
-enum GemvX { X_PLAIN = 0, X_NORM = 1 };
+// X_ATTN: x is the attention output, merged from the decode-attention
+// partials while it is staged (the o projection's prologue)
+enum GemvX { X_PLAIN = 0, X_NORM = 1, X_ATTN = 2 };
 enum GemvEpi { EPI_STORE = 0, EPI_RESID = 1, EPI_QKV = 2, EPI_GU = 3, EPI_HEAD = 4 };
 
 struct GemvArgs {
@@ -30,7 +32,11 @@ struct GemvArgs {
   float *h_out = nullptr;
   // EPI_HEAD: per-block (value, index) argmax partials
   float2 *part = nullptr;       // x = value, y = index bits
+  int part_cap = 0;             // entries `part` holds; a larger grid is refused
   uint32_t *pos_inc = nullptr;  // EPI_HEAD: block 0 increments *pos_inc when set
+  // X_ATTN: partials [nq][attn_nchunks][d + 2] = (o[d], m, l) per chunk
+  const float *attn_part = nullptr;
+  int attn_nchunks = 0, attn_nq = 0;
 };
 
 // Launch the best kernel variant for (m, k, x mode, epilogue); returns the
@@ -45,11 +51,9 @@ struct AttnDecodeArgs {
   const void *kc, *vc;     // this layer's cache [nkv][max_seq][d]
   int kv_bf16, max_seq, nq, nkv, head_dim;
   const uint32_t *pos_ptr; // attends positions 0..*pos_ptr
-  float *part;             // scratch [nq][nchunks][d + 2]
-  unsigned *counters;      // [nkv], zero at rest (the merging block resets it)
-  float *out;              // [nq, d]
+  float *part;             // out: [nq][nchunks][d + 2] per-chunk (o[d], m, l)
 };
-int attn_decode_chunks(int max_seq);
+int attn_decode_chunks(int max_seq, int head_dim);
 size_t attn_decode_part_floats(int nq, int max_seq, int head_dim);
 hipError_t launch_attn_decode(const AttnDecodeArgs &a, hipStream_t s);
 

@@ -87,9 +87,85 @@ __device__ float block_sum(float v, float *scratch4) {
 // applies the RMSNorm there (sum of squares over the whole vector, then
 // g * (x * inv_rms)), which fuses rmsnorm_bf16_weight into the projection.
 
+// the o-projection prologue merges at most this many attention outputs
+// (its LDS holds them)
+constexpr int kMaxAttnMergeK = 16 * kBlock;
+
+// decode attention splits positions into chunks of this many
+__host__ __device__ constexpr int attn_chunk(int d) { return d <= 128 ? 32 : 16; }
+
+// X_ATTN staging: the attention output of head h, lane j is
+//   sum_c w[h][c] o_c[h][j],  w[h][c] = e^(m_c - M_h) / sum_c' e^(m_c' - M_h) l_c'
+// over the chunks c that hold positions <= pos (the split-position softmax
+// recombined; gqa.rs:283-307 is the one-chunk case). All partial loads of a
+// step are independent, so they are issued together.
+__device__ void stage_attn(const GemvArgs &a, float *xs, float *ws) {
+  const int tid = threadIdx.x, d = a.head_dim, nq = a.attn_nq, nch = a.attn_nchunks;
+  const int ch = attn_chunk(d), nv = ((int)*a.pos_ptr + ch) / ch;
+  const size_t sp = (size_t)d + 2;
+  float *ms = ws, *ls = ws + nq * nv;
+  for (int i = tid; i < nq * nv; i += kBlock) {
+    const int h = i / nv, c = i - h * nv;
+    const float *src = a.attn_part + ((size_t)h * nch + c) * sp + d;
+    ms[i] = src[0];
+    ls[i] = src[1];
+  }
+  __syncthreads();
+  for (int h = tid; h < nq; h += kBlock) {
+    float mx = -INFINITY;
+    for (int c = 0; c < nv; c++) mx = fmaxf(mx, ms[h * nv + c]);
+    float l = 0.f;
+    for (int c = 0; c < nv; c++) {
+      const float w = expf(ms[h * nv + c] - mx);
+      ms[h * nv + c] = w;
+      l = fmaf(w, ls[h * nv + c], l);
+    }
+    const float inv = 1.0f / l;
+    for (int c = 0; c < nv; c++) ms[h * nv + c] *= inv;
+  }
+  __syncthreads();
+  // one wavefront per head; lane owns dims j and j + 64; chunk loads are
+  // unrolled by 8 so 16 independent loads are in flight per lane
+  const int lane = tid & 63, wave = tid >> 6;
+  for (int h = wave; h < nq; h += 4) {
+    const float *w = ms + h * nv;
+    const float *base = a.attn_part + (size_t)h * nch * sp;
+    for (int j0 = lane; j0 < d; j0 += 128) {
+      const int j1 = j0 + 64;
+      const bool two = j1 < d;
+      float acc0 = 0.f, acc1 = 0.f;
+      int c = 0;
+      for (; c + 8 <= nv; c += 8) {
+        float v0[8], v1[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+          v0[u] = base[(size_t)(c + u) * sp + j0];
+          v1[u] = two ? base[(size_t)(c + u) * sp + j1] : 0.f;
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+          acc0 = fmaf(w[c + u], v0[u], acc0);
+          acc1 = fmaf(w[c + u], v1[u], acc1);
+        }
+      }
+      for (; c < nv; c++) {
+        acc0 = fmaf(w[c], base[(size_t)c * sp + j0], acc0);
+        if (two) acc1 = fmaf(w[c], base[(size_t)c * sp + j1], acc1);
+      }
+      xs[h * d + j0] = acc0;
+      if (two) xs[h * d + j1] = acc1;
+    }
+  }
+}
+
 template <int XM>
 __device__ void stage_x(const GemvArgs &a, float *xs, float *red4) {
   const int k = a.k, tid = threadIdx.x;
+  if (XM == X_ATTN) {
+    stage_attn(a, xs, xs + ((k + 3) & ~3));
+    __syncthreads();
+    return;
+  }
   float ss = 0.f;
   for (int j = tid * 4; j < k; j += kBlock * 4) {
     float4 v = *(const float4 *)(a.x + j);
@@ -274,10 +350,14 @@ __global__ void __launch_bounds__(kBlock) gemv_generic_kernel(GemvArgs a) {
   if (EPI == EPI_QKV) pos = *a.pos_ptr;
   // scalar staging (k may not be a multiple of 4)
   float ss = 0.f;
-  for (int j = tid; j < k; j += kBlock) {
-    float v = a.x[j];
-    xs[j] = v;
-    ss += v * v;
+  if (XM == X_ATTN) {
+    stage_attn(a, xs, xs + ((k + 3) & ~3));
+  } else {
+    for (int j = tid; j < k; j += kBlock) {
+      float v = a.x[j];
+      xs[j] = v;
+      ss += v * v;
+    }
   }
   if (XM == X_NORM) {
     float tot = block_sum(ss, red4);
@@ -313,99 +393,96 @@ __global__ void __launch_bounds__(kBlock) gemv_generic_kernel(GemvArgs a) {
 
 // ------------------------------------------------------ decode attention ---
 //
-// Workgroup (kv head g, chunk c of kAttnChunk positions) scores the chunk for
-// the q_per_kv query heads that share g (K/V read once per group), keeps a
+// Workgroup (kv head g, chunk c of attn_chunk(d) positions) scores the chunk
+// for the q_per_kv query heads that share g (K/V read once per group), keeps a
 // chunk-local softmax (max m, sum l, unnormalised mix o), and the last
 // workgroup of the group to finish (atomic counter) merges the chunks:
 // y = sum_c e^(m_c - M) o_c / sum_c e^(m_c - M) l_c. The serial reference
-// (gqa.rs:174-218) is the same quantity with one chunk.
-constexpr int kAttnChunk = 64;
+// (gqa.rs:174-218) is the same quantity with one chunk. K, V (chunk x d each)
+// and q stay under the 64 KiB workgroup LDS limit: 32 positions up to d = 128,
+// 16 up to d = 256.
 constexpr int kMaxQPerKv = 8;
 constexpr int kMaxHeadDim = 256;
 
 __global__ void __launch_bounds__(kBlock) attn_decode_kernel(AttnDecodeArgs a) {
   extern __shared__ float smem[];
-  const int d = a.head_dim, gq = a.nq / a.nkv, dp = d + 1;
+  const int d = a.head_dim, gq = a.nq / a.nkv, dp = d + 1, ch = attn_chunk(d);
   float *q_s = smem;                        // [gq][d]
   float *k_s = q_s + gq * d;                // [chunk][d + 1]
-  float *v_s = k_s + kAttnChunk * dp;       // [chunk][d]
-  float *p_s = v_s + kAttnChunk * d;        // [gq][chunk]
-  float *ml_s = p_s + gq * kAttnChunk;      // [gq][2]
-  __shared__ int is_last;
+  float *v_s = k_s + ch * dp;               // [chunk][d]
+  float *p_s = v_s + ch * d;                // [gq][chunk]
+  float *ml_s = p_s + gq * ch;              // [gq][2]
   const int g = blockIdx.x, c = blockIdx.y, nchunks = gridDim.y, tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int seq = (int)*a.pos_ptr + 1;
-  const int t0 = c * kAttnChunk;
-  const int n = min(kAttnChunk, seq - t0);
+  const int t0 = c * ch;
+  const int n = min(ch, seq - t0);
+  if (n <= 0) return;  // past the cursor: the o-projection merges chunks < seq only
   const float scale = 1.0f / sqrtf((float)d);
-  const size_t stride_part = (size_t)d + 2;
-  if (n > 0) {
-    for (int i = tid; i < gq * d; i += kBlock) q_s[i] = a.q[(size_t)g * gq * d + i];
-    const size_t kv0 = ((size_t)g * a.max_seq + t0) * d;
+  for (int i = tid; i < gq * d; i += kBlock) q_s[i] = a.q[(size_t)g * gq * d + i];
+  const size_t kv0 = ((size_t)g * a.max_seq + t0) * d;
+  if (!a.kv_bf16 && (d & 3) == 0) {
+    const float4 *k4 = (const float4 *)((const float *)a.kc + kv0);
+    const float4 *v4 = (const float4 *)((const float *)a.vc + kv0);
+    for (int i = tid; i < (n * d) >> 2; i += kBlock) {
+      const float4 kv = k4[i], vv = v4[i];
+      const int e = i << 2, t = e / d, j = e - t * d;
+      float *kd = k_s + t * dp + j;
+      kd[0] = kv.x;
+      kd[1] = kv.y;
+      kd[2] = kv.z;
+      kd[3] = kv.w;
+      *(float4 *)(v_s + e) = vv;
+    }
+  } else {
     for (int i = tid; i < n * d; i += kBlock) {
       const int t = i / d, j = i - t * d;
       k_s[t * dp + j] = load_kv(a.kc, kv0 + i, a.kv_bf16);
       v_s[i] = load_kv(a.vc, kv0 + i, a.kv_bf16);
     }
-    __syncthreads();
-    for (int i = tid; i < gq * n; i += kBlock) {
-      const int h = i / n, t = i - h * n;
-      const float *qh = q_s + h * d, *kt = k_s + t * dp;
-      float s = 0.f;
-      for (int j = 0; j < d; j++) s = fmaf(qh[j], kt[j], s);
-      p_s[h * kAttnChunk + t] = s * scale;
-    }
-    __syncthreads();
-    for (int h = wave; h < gq; h += 4) {
-      float s = lane < n ? p_s[h * kAttnChunk + lane] : -INFINITY;
-      const float mx = group_max<kWave>(s);
-      const float e = lane < n ? expf(s - mx) : 0.f;
-      const float l = group_sum<kWave>(e);
-      if (lane < n) p_s[h * kAttnChunk + lane] = e;
-      if (lane == 0) {
-        ml_s[2 * h] = mx;
-        ml_s[2 * h + 1] = l;
-      }
-    }
-    __syncthreads();
-    for (int i = tid; i < gq * d; i += kBlock) {
-      const int h = i / d, j = i - h * d;
-      const float *ph = p_s + h * kAttnChunk;
-      float o = 0.f;
-      for (int t = 0; t < n; t++) o = fmaf(ph[t], v_s[t * d + j], o);
-      float *dst = a.part + ((size_t)(g * gq + h) * nchunks + c) * stride_part;
-      dst[j] = o;
-      if (j == 0) {
-        dst[d] = ml_s[2 * h];
-        dst[d + 1] = ml_s[2 * h + 1];
-      }
-    }
-  }
-  // publish this chunk, elect the group's last workgroup to merge
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) {
-    unsigned prev = atomicAdd(&a.counters[g], 1u);
-    is_last = prev == (unsigned)(nchunks - 1);
   }
   __syncthreads();
-  if (!is_last) return;
-  __threadfence();
-  const int nvalid = (seq + kAttnChunk - 1) / kAttnChunk;
+  for (int i = tid; i < gq * n; i += kBlock) {
+    const int h = i / n, t = i - h * n;
+    const float *qh = q_s + h * d, *kt = k_s + t * dp;
+    float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+    int j = 0;
+#pragma unroll 4
+    for (; j + 3 < d; j += 4) {
+      s0 = fmaf(qh[j], kt[j], s0);
+      s1 = fmaf(qh[j + 1], kt[j + 1], s1);
+      s2 = fmaf(qh[j + 2], kt[j + 2], s2);
+      s3 = fmaf(qh[j + 3], kt[j + 3], s3);
+    }
+    for (; j < d; j++) s0 = fmaf(qh[j], kt[j], s0);
+    p_s[h * ch + t] = ((s0 + s1) + (s2 + s3)) * scale;
+  }
+  __syncthreads();
+  for (int h = wave; h < gq; h += 4) {
+    float s = lane < n ? p_s[h * ch + lane] : -INFINITY;
+    const float mx = group_max<kWave>(s);
+    const float e = lane < n ? expf(s - mx) : 0.f;
+    const float l = group_sum<kWave>(e);
+    if (lane < n) p_s[h * ch + lane] = e;
+    if (lane == 0) {
+      ml_s[2 * h] = mx;
+      ml_s[2 * h + 1] = l;
+    }
+  }
+  __syncthreads();
+  const size_t stride_part = (size_t)d + 2;
   for (int i = tid; i < gq * d; i += kBlock) {
     const int h = i / d, j = i - h * d;
-    const float *src = a.part + (size_t)(g * gq + h) * nchunks * stride_part;
-    float mx = -INFINITY;
-    for (int cc = 0; cc < nvalid; cc++) mx = fmaxf(mx, src[cc * stride_part + d]);
-    float l = 0.f, o = 0.f;
-    for (int cc = 0; cc < nvalid; cc++) {
-      const float w = expf(src[cc * stride_part + d] - mx);
-      l = fmaf(w, src[cc * stride_part + d + 1], l);
-      o = fmaf(w, src[cc * stride_part + j], o);
+    const float *ph = p_s + h * ch;
+    float o = 0.f;
+    for (int t = 0; t < n; t++) o = fmaf(ph[t], v_s[t * d + j], o);
+    float *dst = a.part + ((size_t)(g * gq + h) * nchunks + c) * stride_part;
+    dst[j] = o;
+    if (j == 0) {
+      dst[d] = ml_s[2 * h];
+      dst[d + 1] = ml_s[2 * h + 1];
     }
-    a.out[(size_t)(g * gq + h) * d + j] = o / l;
   }
-  if (tid == 0) a.counters[g] = 0u;
 }
 
 // ----------------------------------------------------------- small ops ----
@@ -552,12 +629,20 @@ __global__ void __launch_bounds__(1024) argmax_final_kernel(ArgmaxFinalArgs a) {
   uint32_t bi = 0xffffffffu;
   const bool forced = a.state && a.state[3] == 1u;
   if (!forced) {
-    for (int i = threadIdx.x; i < a.nparts; i += blockDim.x) {
-      const float2 p = a.part[i];
-      if (beats(p.x, __float_as_uint(p.y), bv, bi)) {
-        bv = p.x;
-        bi = __float_as_uint(p.y);
+    // 8 partials per thread per round, all loaded before any compare
+    for (int i0 = threadIdx.x; i0 < a.nparts; i0 += blockDim.x * 8) {
+      float2 p[8];
+#pragma unroll
+      for (int u = 0; u < 8; u++) {
+        const int i = i0 + u * (int)blockDim.x;
+        p[u] = i < a.nparts ? a.part[i] : make_float2(-INFINITY, __uint_as_float(0xffffffffu));
       }
+#pragma unroll
+      for (int u = 0; u < 8; u++)
+        if (beats(p[u].x, __float_as_uint(p[u].y), bv, bi)) {
+          bv = p[u].x;
+          bi = __float_as_uint(p[u].y);
+        }
     }
     float2 b = block_best(bv, bi, sh);
     if (threadIdx.x == 0) {
@@ -651,7 +736,8 @@ __global__ void __launch_bounds__(kBlock) gemm_mfma_kernel(GemmArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int n0 = blockIdx.x * GBN, m0 = blockIdx.y * GBM;
   const int M = a.M, N = a.N, K = a.K;
-  const bool vec = (K & 7) == 0;
+  // 16-byte operand loads need K % 8 == 0 and 16-byte aligned bases
+  const bool vec = (K & 7) == 0 && (((uintptr_t)a.a_hi | (uintptr_t)a.a_lo | (uintptr_t)a.w) & 15) == 0;
   f32x16 acc0, acc1;
 #pragma unroll
   for (int i = 0; i < 16; i++) {
@@ -823,13 +909,22 @@ inline unsigned nblk(size_t n, unsigned b) { return (unsigned)((n + b - 1) / b);
 // ============================================================ launchers ====
 
 namespace {
+// dynamic LDS of a GEMV launch: x (k floats, rounded to 4) + the X_ATTN
+// merge weights (2 per head and chunk)
+size_t stage_bytes(const GemvArgs &a, int xm) {
+  size_t n = (size_t)((a.k + 3) & ~3);
+  if (xm == X_ATTN) n += 2 * (size_t)a.attn_nq * a.attn_nchunks;
+  return n * sizeof(float);
+}
+
 template <int TEAM, int ROWS, int CPT, int XM, int EPI>
 hipError_t go_gemv(const GemvArgs &a, hipStream_t s, int *nparts) {
   const int rows_per_block = ROWS * (kBlock / TEAM);
   const unsigned grid = nblk((size_t)a.m, rows_per_block);
   if (nparts) *nparts = (int)grid;
+  if (EPI == EPI_HEAD && (int)grid > a.part_cap) return hipErrorInvalidValue;
   hipLaunchKernelGGL((gemv_kernel<TEAM, ROWS, CPT, XM, EPI>), dim3(grid), dim3(kBlock),
-                     (size_t)a.k * sizeof(float), s, a);
+                     stage_bytes(a, XM), s, a);
   return hipGetLastError();
 }
 
@@ -837,8 +932,9 @@ template <int XM, int EPI>
 hipError_t go_gemv_generic(const GemvArgs &a, hipStream_t s, int *nparts) {
   const unsigned grid = nblk((size_t)a.m, 8);
   if (nparts) *nparts = (int)grid;
+  if (EPI == EPI_HEAD && (int)grid > a.part_cap) return hipErrorInvalidValue;
   hipLaunchKernelGGL((gemv_generic_kernel<XM, EPI>), dim3(grid), dim3(kBlock),
-                     (size_t)((a.k + 3) & ~3) * sizeof(float), s, a);
+                     stage_bytes(a, XM), s, a);
   return hipGetLastError();
 }
 
@@ -882,8 +978,10 @@ hipError_t pick_gemv(const GemvArgs &a, hipStream_t s, int *nparts) {
 
 hipError_t launch_gemv(const GemvArgs &a, GemvX xm, GemvEpi epi, hipStream_t s, int *nparts) {
   if (a.m <= 0) return hipSuccess;
+  if (xm == X_ATTN && a.k > kMaxAttnMergeK) return hipErrorInvalidValue;
   if (xm == X_PLAIN && epi == EPI_STORE) return pick_gemv<X_PLAIN, EPI_STORE>(a, s, nparts);
   if (xm == X_PLAIN && epi == EPI_RESID) return pick_gemv<X_PLAIN, EPI_RESID>(a, s, nparts);
+  if (xm == X_ATTN && epi == EPI_RESID) return pick_gemv<X_ATTN, EPI_RESID>(a, s, nparts);
   if (xm == X_NORM && epi == EPI_QKV) return pick_gemv<X_NORM, EPI_QKV>(a, s, nparts);
   if (xm == X_NORM && epi == EPI_GU) return pick_gemv<X_NORM, EPI_GU>(a, s, nparts);
   if (xm == X_NORM && epi == EPI_HEAD) return pick_gemv<X_NORM, EPI_HEAD>(a, s, nparts);
@@ -898,19 +996,22 @@ int gemv_head_parts(int m, int k) {
   return (int)nblk((size_t)m, 2);
 }
 
-int attn_decode_chunks(int max_seq) { return (max_seq + kAttnChunk - 1) / kAttnChunk; }
+int attn_decode_chunks(int max_seq, int head_dim) {
+  return (max_seq + attn_chunk(head_dim) - 1) / attn_chunk(head_dim);
+}
 
 size_t attn_decode_part_floats(int nq, int max_seq, int head_dim) {
-  return (size_t)nq * attn_decode_chunks(max_seq) * ((size_t)head_dim + 2);
+  return (size_t)nq * attn_decode_chunks(max_seq, head_dim) * ((size_t)head_dim + 2);
 }
 
 hipError_t launch_attn_decode(const AttnDecodeArgs &a, hipStream_t s) {
   const int gq = a.nq / a.nkv, d = a.head_dim;
   if (gq > kMaxQPerKv || d > kMaxHeadDim) return hipErrorInvalidValue;
-  const size_t smem =
-      sizeof(float) * ((size_t)gq * d + (size_t)kAttnChunk * (d + 1) + (size_t)kAttnChunk * d +
-                       (size_t)gq * kAttnChunk + 2 * gq);
-  dim3 grid(a.nkv, attn_decode_chunks(a.max_seq));
+  const int ch = attn_chunk(d);
+  const size_t smem = sizeof(float) * ((size_t)gq * d + (size_t)ch * (d + 1) + (size_t)ch * d +
+                                       (size_t)gq * ch + 2 * gq);
+  if (smem > 65536) return hipErrorInvalidValue;
+  dim3 grid(a.nkv, attn_decode_chunks(a.max_seq, d));
   hipLaunchKernelGGL(attn_decode_kernel, grid, dim3(kBlock), smem, s, a);
   return hipGetLastError();
 }
@@ -1032,8 +1133,8 @@ hipError_t launch_permute_rows(uint16_t *dst, const uint16_t *src, const int *pe
 
 const char *kernel_build_info() {
   return "gfx950; gemv: wave/workgroup teams, 16B nontemporal bf16 loads, fused "
-         "rmsnorm/bias+rope+kv/swiglu/residual/argmax epilogues; attention: split-K "
-         "decode with last-block merge; prefill: v_mfma_f32_32x32x16_bf16 hi/lo GEMM";
+         "rmsnorm/bias+rope+kv/swiglu/residual/argmax epilogues; attention: split-position "
+         "decode partials merged in the o-projection prologue; prefill: v_mfma_f32_32x32x16_bf16 hi/lo GEMM";
 }
 
 }  // namespace myos

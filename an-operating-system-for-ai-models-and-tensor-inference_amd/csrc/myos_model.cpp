@@ -69,7 +69,6 @@ struct myos_model {
         *normed = nullptr, *attn_part = nullptr;
   float2 *part = nullptr;
   int nparts = 0;
-  unsigned *counters = nullptr;
   uint32_t *state = nullptr, *out_ids = nullptr;
   uint32_t *host_state = nullptr;  // pinned [4]
   // prefill workspace, grown on demand
@@ -80,7 +79,8 @@ struct myos_model {
   uint32_t *ptok = nullptr;
   // graph + timing
   bool use_graph = true;
-  hipGraphExec_t graph = nullptr;
+  hipGraphExec_t graph = nullptr;   // one decode step
+  hipGraphExec_t graph_n = nullptr; // kGraphSteps decode steps back to back
   hipEvent_t ev0 = nullptr, ev1 = nullptr;
   double prefill_ms = 0, decode_ms = 0;
 
@@ -202,17 +202,19 @@ int enq_kernel(myos_model *m, int which, size_t l, bool advance_pos) {
       ad.head_dim = (int)s.head_dim;
       ad.pos_ptr = m->state;
       ad.part = m->attn_part;
-      ad.counters = m->counters;
-      ad.out = m->att;
       return hs(launch_attn_decode(ad, st));
     }
     case MYOS_K_O:
       g.w = L.wo;
-      g.x = m->att;
+      g.attn_part = m->attn_part;
+      g.attn_nchunks = attn_decode_chunks((int)m->max_seq, (int)s.head_dim);
+      g.attn_nq = (int)s.num_q_heads;
+      g.head_dim = (int)s.head_dim;
+      g.pos_ptr = m->state;
       g.m = (int)s.hidden;
       g.k = (int)m->q_dim;
       g.y = m->x;
-      return hs(launch_gemv(g, X_PLAIN, EPI_RESID, st));
+      return hs(launch_gemv(g, X_ATTN, EPI_RESID, st));
     case MYOS_K_GATE_UP:
       g.w = L.wgu;
       g.x = m->x;
@@ -238,6 +240,7 @@ int enq_kernel(myos_model *m, int which, size_t l, bool advance_pos) {
       g.k = (int)s.hidden;
       g.y = m->logits;
       g.part = m->part;
+      g.part_cap = m->nparts;
       g.normed_out = m->normed;
       g.pos_inc = advance_pos ? m->state : nullptr;
       return hs(launch_gemv(g, X_NORM, EPI_HEAD, st));
@@ -268,27 +271,52 @@ int enqueue_step(myos_model *m) {
   return enq_kernel(m, MYOS_K_HEAD, 0, true);
 }
 
+// Decode steps replay from graphs: one holding a single step and one holding
+// kGraphSteps steps, so a long greedy decode pays one graph launch per
+// kGraphSteps tokens (every step reads its position/token from device state).
+constexpr size_t kGraphSteps = 8;
+
+hipGraphExec_t capture_steps(myos_model *m, size_t steps) {
+  hipGraph_t g = nullptr;
+  hipGraphExec_t ge = nullptr;
+  if (hipStreamBeginCapture(m->stream, hipStreamCaptureModeThreadLocal) == hipSuccess) {
+    int rc = MYOS_OK;
+    for (size_t i = 0; i < steps && rc == MYOS_OK; i++) rc = enqueue_step(m);
+    hipError_t e = hipStreamEndCapture(m->stream, &g);
+    if (rc == MYOS_OK && e == hipSuccess && g) {
+      if (hipGraphInstantiate(&ge, g, nullptr, nullptr, 0) != hipSuccess) ge = nullptr;
+    }
+    if (g) (void)hipGraphDestroy(g);
+  }
+  (void)hipGetLastError();
+  return ge;
+}
+
 void prepare_graph(myos_model *m) {
   if (m->use_graph && !m->graph) {
-    hipGraph_t g = nullptr;
-    if (hipStreamBeginCapture(m->stream, hipStreamCaptureModeThreadLocal) == hipSuccess) {
-      int rc = enqueue_step(m);
-      hipError_t e = hipStreamEndCapture(m->stream, &g);
-      if (rc == MYOS_OK && e == hipSuccess && g) {
-        if (hipGraphInstantiate(&m->graph, g, nullptr, nullptr, 0) != hipSuccess)
-          m->graph = nullptr;
-      }
-      if (g) (void)hipGraphDestroy(g);
-    }
-    (void)hipGetLastError();
+    m->graph = capture_steps(m, 1);
+    if (m->graph) m->graph_n = capture_steps(m, kGraphSteps);
     if (!m->graph) m->use_graph = false;  // capture failed: plain launches from here on
   }
 }
 
-int run_step(myos_model *m) {
+// run n decode steps on the model stream
+int run_steps(myos_model *m, size_t n) {
   prepare_graph(m);
-  if (m->use_graph && m->graph) return hs(hipGraphLaunch(m->graph, m->stream));
-  return enqueue_step(m);
+  while (n) {
+    if (m->use_graph && m->graph_n && n >= kGraphSteps) {
+      HIP_TRY(hipGraphLaunch(m->graph_n, m->stream));
+      n -= kGraphSteps;
+    } else if (m->use_graph && m->graph) {
+      HIP_TRY(hipGraphLaunch(m->graph, m->stream));
+      n -= 1;
+    } else {
+      int rc = enqueue_step(m);
+      if (rc) return rc;
+      n -= 1;
+    }
+  }
+  return MYOS_OK;
 }
 
 int write_state(myos_model *m, uint32_t pos, uint32_t token, uint32_t step, uint32_t mode) {
@@ -342,6 +370,7 @@ int validate_shape(const myos_block_shape *s, size_t max_seq) {
   // device limits of this build: q heads per kv head <= 8, head_dim <= 256,
   // 32-bit row indices
   if (s->num_q_heads / s->num_kv_heads > 8 || s->head_dim > 256) return MYOS_E_SHAPE;
+  if (s->num_q_heads * s->head_dim > 4096) return MYOS_E_SHAPE;  // o-projection merge width
   if (s->vocab > (1u << 30) || s->hidden > (1u << 20) || s->intermediate > (1u << 24) ||
       max_seq > (1u << 24))
     return MYOS_E_SHAPE;
@@ -384,6 +413,7 @@ void myos_model_close(myos_model *m) {
   if (!m) return;
   if (m->stream) (void)hipStreamSynchronize(m->stream);
   if (m->graph) (void)hipGraphExecDestroy(m->graph);
+  if (m->graph_n) (void)hipGraphExecDestroy(m->graph_n);
   if (m->ev0) (void)hipEventDestroy(m->ev0);
   if (m->ev1) (void)hipEventDestroy(m->ev1);
   if (m->wbuf) (void)hipFree(m->wbuf);
@@ -575,9 +605,9 @@ static int open_impl(myos_model *m, const char *path, const myos_block_shape *sh
   const size_t b_lg = align256(V * 4), b_part = align256(m->nparts * sizeof(float2));
   const size_t b_ap =
       align256(attn_decode_part_floats((int)s.num_q_heads, (int)max_seq, (int)s.head_dim) * 4);
-  const size_t b_cnt = align256(s.num_kv_heads * 4), b_st = align256(16);
+  const size_t b_st = align256(16);
   const size_t b_ids = align256(max_seq * 4);
-  m->ws_bytes = 2 * b_x + 2 * b_q + b_h + b_lg + b_part + b_ap + b_cnt + b_st + b_ids;
+  m->ws_bytes = 2 * b_x + 2 * b_q + b_h + b_lg + b_part + b_ap + b_st + b_ids;
   HIP_TRY(hipMalloc((void **)&m->ws, m->ws_bytes));
   HIP_TRY(hipMemsetAsync(m->ws, 0, m->ws_bytes, m->stream));
   p = m->ws;
@@ -597,8 +627,6 @@ static int open_impl(myos_model *m, const char *path, const myos_block_shape *sh
   p += b_part;
   m->attn_part = (float *)p;
   p += b_ap;
-  m->counters = (unsigned *)p;
-  p += b_cnt;
   m->state = (uint32_t *)p;
   p += b_st;
   m->out_ids = (uint32_t *)p;
@@ -729,6 +757,7 @@ int myos_prefill(myos_model *m, const uint32_t *tokens, size_t n) {
   hd.k = H;
   hd.y = m->logits;
   hd.part = m->part;
+  hd.part_cap = m->nparts;
   hd.normed_out = m->normed;
   HIP_TRY(launch_gemv(hd, X_NORM, EPI_HEAD, st));
   HIP_TRY(hipEventRecord(m->ev1, st));
@@ -750,7 +779,7 @@ int myos_forward_token(myos_model *m, uint32_t token, size_t pos) {
   if ((size_t)token >= m->s.vocab) return MYOS_E_TOKEN;
   int rc = write_state(m, (uint32_t)pos, token, 0, 1);
   if (rc) return rc;
-  rc = run_step(m);
+  rc = run_steps(m, 1);
   if (rc) return rc;
   HIP_TRY(hipStreamSynchronize(m->stream));
   m->len += 1;
@@ -767,10 +796,8 @@ int myos_greedy_decode(myos_model *m, size_t steps, uint32_t *out) {
     int rc = write_state(m, (uint32_t)m->len, 0, 0, 0);
     if (rc) return rc;
     HIP_TRY(hipEventRecord(m->ev0, m->stream));
-    for (size_t i = 0; i < n; i++) {
-      rc = run_step(m);
-      if (rc) return rc;
-    }
+    rc = run_steps(m, n);
+    if (rc) return rc;
     HIP_TRY(hipEventRecord(m->ev1, m->stream));
     HIP_TRY(hipStreamSynchronize(m->stream));
     HIP_TRY(hipMemcpy(out, m->out_ids, n * 4, hipMemcpyDeviceToHost));
@@ -797,6 +824,20 @@ int myos_time_kernel(myos_model *m, int which, int reps, double *avg_ms) {
   int rc = write_state(m, pos, 0, 0, 0);
   if (rc) return rc;
   const size_t n = which == MYOS_K_HEAD ? 1 : m->s.num_layers;
+  if (!m->use_graph) {
+    // plain launches (for tools that do not follow graph replays)
+    for (size_t l = 0; l < n && !rc; l++) rc = enq_kernel(m, which, l, false);  // warm
+    if (!rc) rc = hs(hipEventRecord(m->ev0, m->stream));
+    for (int r = 0; r < reps && !rc; r++)
+      for (size_t l = 0; l < n && !rc; l++) rc = enq_kernel(m, which, l, false);
+    if (!rc) rc = hs(hipEventRecord(m->ev1, m->stream));
+    if (!rc) rc = hs(hipStreamSynchronize(m->stream));
+    float ms = 0;
+    if (!rc) rc = hs(hipEventElapsedTime(&ms, m->ev0, m->ev1));
+    if (rc) return rc;
+    *avg_ms = (double)ms / ((double)reps * (double)n);
+    return MYOS_OK;
+  }
   hipGraph_t g = nullptr;
   hipGraphExec_t ge = nullptr;
   HIP_TRY(hipStreamBeginCapture(m->stream, hipStreamCaptureModeThreadLocal));
