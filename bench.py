@@ -172,9 +172,15 @@ def main():
                                 for n, v in kernels.items()))
     dom = kernels["gate_up_swiglu"]
     achieved = dom["bytes"] / (dom["avg_us"] * 1e-6)
+    # HBM bytes per launch from the calibrated FETCH_SIZE / WRITE_SIZE passes
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "decode_traffic_qwen25_1_5b.json")
+    if os.path.exists(tpath) and kv == myos.KV_F32:
+        traffic = json.load(open(tpath))["traffic_bytes_per_launch"].get("gate_up_swiglu")
     roofline = {"bound": "hbm", "kernel": "gate_up_swiglu (fused rmsnorm + gate/up GEMV + SwiGLU)",
                 "achieved": round(achieved / 1e9, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK, 4), "traffic": None}
+                "frac": round(achieved / HBM_PEAK, 4), "traffic": traffic,
+                "algorithmic_bytes": dom["bytes"]}
     m.close()
 
     cpu = None
