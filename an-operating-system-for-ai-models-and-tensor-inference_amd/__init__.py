@@ -35,6 +35,7 @@ KIND = {
 }
 
 KV_F32, KV_BF16 = 0, 1
+DECODE_AUTO, DECODE_KERNELS, DECODE_PERSISTENT = 0, 1, 2
 SHAPE_QWEN25_1_5B, SHAPE_QWEN25_7B = 0, 1
 
 
@@ -85,6 +86,10 @@ EXPORTS = {
     "myos_copy_normed": ([P, P, SZ], I32),
     "myos_kv_read": ([P, SZ, SZ, SZ, P, P], I32),
     "myos_set_graph": ([P, I32], I32),
+    "myos_set_decode_mode": ([P, I32], I32),
+    "myos_decode_path": ([P], I32),
+    "myos_set_decode_trace": ([P, C.c_int64], I32),
+    "myos_copy_decode_trace": ([P, P, SZ], I32),
     "myos_last_prefill_ms": ([P], C.c_double),
     "myos_last_decode_ms": ([P], C.c_double),
     "myos_weight_bytes": ([P], SZ),
@@ -362,6 +367,27 @@ class Model:
 
     def set_graph(self, on: bool):
         _check(lib().myos_set_graph(self._h, 1 if on else 0), "set_graph")
+
+    def set_decode_mode(self, mode: int):
+        """DECODE_AUTO / DECODE_KERNELS / DECODE_PERSISTENT for greedy_decode."""
+        _check(lib().myos_set_decode_mode(self._h, int(mode)), "set_decode_mode")
+
+    def set_decode_trace(self, step: int):
+        """Record phase timestamps of decode step `step` of each persistent
+        greedy_decode call (step < 0: off)."""
+        _check(lib().myos_set_decode_trace(self._h, int(step)), "set_decode_trace")
+
+    def decode_trace(self):
+        """[256 workgroups, 5 * layers + 3] device clock ticks (100 MHz)."""
+        import numpy as np
+        out = np.zeros((256, 5 * self.shape.num_layers + 3), np.uint64)
+        _check(lib().myos_copy_decode_trace(self._h, out.ctypes.data_as(P), out.size),
+               "copy_decode_trace")
+        return out
+
+    def decode_path(self) -> int:
+        """DECODE_KERNELS or DECODE_PERSISTENT: the path greedy_decode takes."""
+        return int(lib().myos_decode_path(self._h))
 
     def last_prefill_ms(self) -> float:
         return float(lib().myos_last_prefill_ms(self._h))

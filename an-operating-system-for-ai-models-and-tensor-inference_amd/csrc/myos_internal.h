@@ -84,6 +84,7 @@ struct ArgmaxFinalArgs {
   const uint16_t *embed = nullptr;
   float *x = nullptr;
   int hidden = 0;
+  uint32_t vocab = 0;                  // indices >= vocab (none found) select id 0
 };
 hipError_t launch_argmax_final(const ArgmaxFinalArgs &a, hipStream_t s);
 
@@ -123,6 +124,45 @@ hipError_t launch_attn_prefill(const AttnPrefillArgs &a, hipStream_t s);
 
 hipError_t launch_permute_rows(uint16_t *dst, const uint16_t *src, const int *perm, int rows,
                                int cols, hipStream_t s);
+
+// ---- persistent decode (myos_persistent.hip) ---------------------------------
+// One cooperative launch runs `steps` greedy decode steps. Workgroups hand
+// activations to each other as 64-bit (value, tag) words written and read with
+// device-coherent (sc1) accesses; a consumer waits for exactly the words it
+// needs to carry the expected tag, so there is no grid barrier or fence.
+struct PersistLayer {
+  const uint16_t *ln1, *wqkv, *wo, *ln2, *wgu, *wd;
+  const float *bqkv;
+};
+struct PersistArgs {
+  int H, I, V, L, nq, nkv, d, max_seq, qkv_rows;
+  float eps;
+  const PersistLayer *layers;  // device array [L]
+  const uint16_t *embed, *final_norm, *head;
+  const float2 *rope;
+  float *kc, *vc;              // f32 cache base, layer stride = layer_kv
+  size_t layer_kv;
+  // tagged exchange buffers (zeroed once; tags only grow)
+  uint64_t *tq, *tkv, *tpart, *txo, *th, *txd, *targ;
+  // outputs
+  float *logits, *normed, *x_out;
+  float2 *part_out;
+  int part_cap;
+  const float2 *part_in;       // argmax partials of the forward before the launch
+  int nparts_in;
+  uint32_t *state, *out_ids;
+  uint32_t *err;
+  uint32_t tag_base, steps, pos0;
+  int lds_wd;                  // set by the launcher: LDS offset (floats) of the down rows
+  uint64_t *trace;             // optional [grid][5 L + 3] phase timestamps of one step
+  uint32_t trace_step;
+};
+int persist_grid();                       // workgroups per launch
+int persist_tags_per_step(int layers);
+size_t persist_part_words(int nq, int max_seq, int d);
+bool persist_supported(int H, int I, int qdim, int d, int gq);
+bool persist_device_ok(const PersistArgs &a);  // shape, LDS and the current device fit
+hipError_t launch_decode_persistent(const PersistArgs &a, hipStream_t s);
 
 const char *kernel_build_info();
 

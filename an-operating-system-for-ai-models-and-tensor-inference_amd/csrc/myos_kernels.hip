@@ -647,7 +647,7 @@ __global__ void __launch_bounds__(1024) argmax_final_kernel(ArgmaxFinalArgs a) {
     float2 b = block_best(bv, bi, sh);
     if (threadIdx.x == 0) {
       uint32_t idx = __float_as_uint(b.y);
-      tok_s = idx == 0xffffffffu ? 0u : idx;
+      tok_s = idx < a.vocab ? idx : 0u;  // no candidate (all NaN / -inf) -> 0
     }
   } else if (threadIdx.x == 0) {
     tok_s = a.state[1];

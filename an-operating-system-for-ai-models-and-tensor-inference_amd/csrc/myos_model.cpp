@@ -18,6 +18,9 @@
 //
 // A decode step is 2 + 5 * layers launches, all reading the device-resident
 // state {pos, token, step, mode}, so one captured hipGraph replays every step.
+// greedy_decode instead runs the whole call as one persistent cooperative
+// kernel (myos_persistent.hip) when the shape, an f32 cache and the device
+// allow it; both paths leave the same state, logits and cache behind.
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <string.h>
@@ -83,6 +86,17 @@ struct myos_model {
   hipGraphExec_t graph_n = nullptr; // kGraphSteps decode steps back to back
   hipEvent_t ev0 = nullptr, ev1 = nullptr;
   double prefill_ms = 0, decode_ms = 0;
+  // persistent decode: one cooperative launch per greedy_decode call
+  int decode_mode = MYOS_DECODE_AUTO;
+  bool persist_ok = false;        // shape, KV dtype and device allow it
+  uint8_t *pbuf = nullptr;        // tagged exchange words + error word, zeroed
+  size_t pbuf_bytes = 0;
+  PersistLayer *dlayers = nullptr;
+  PersistArgs pargs{};            // all but tag_base / steps / pos0
+  uint32_t tag_base = 1;          // tags below this value are spent
+  uint32_t *err = nullptr;
+  uint64_t *trace = nullptr;      // phase timestamps (myos_set_decode_trace)
+  int64_t trace_step = -1;
 
   void *kc_layer(size_t l) const {
     return kc + l * layer_kv_elems * (kv_bf16 ? 2 : 4);
@@ -261,6 +275,7 @@ int enqueue_step(myos_model *m) {
   af.embed = m->embed;
   af.x = m->x;
   af.hidden = (int)m->s.hidden;
+  af.vocab = (uint32_t)m->s.vocab;
   HIP_TRY(launch_argmax_final(af, m->stream));
   static const int order[5] = {MYOS_K_QKV, MYOS_K_ATTN, MYOS_K_O, MYOS_K_GATE_UP, MYOS_K_DOWN};
   for (size_t l = 0; l < m->s.num_layers; l++)
@@ -377,6 +392,114 @@ int validate_shape(const myos_block_shape *s, size_t max_seq) {
   return MYOS_OK;
 }
 
+// Persistent decode buffers, when the shape, the f32 cache and the device fit
+// the cooperative kernel: tagged words for q, this step's k/v, attention
+// partials, the residual after o and after down, h, and the head's argmax
+// partials; all zero, so no tag >= 1 matches before it is written.
+int setup_persistent(myos_model *m) {
+  const myos_block_shape &s = m->s;
+  PersistArgs &a = m->pargs;
+  a.H = (int)s.hidden;
+  a.I = (int)s.intermediate;
+  a.V = (int)s.vocab;
+  a.L = (int)s.num_layers;
+  a.nq = (int)s.num_q_heads;
+  a.nkv = (int)s.num_kv_heads;
+  a.d = (int)s.head_dim;
+  a.max_seq = (int)m->max_seq;
+  a.qkv_rows = (int)m->qkv_rows;
+  a.eps = s.rms_eps;
+  if (m->kv_bf16 || !persist_device_ok(a)) return MYOS_OK;  // per-kernel path only
+  const size_t words[7] = {m->q_dim, 2 * m->kv_dim,
+                           persist_part_words(a.nq, a.max_seq, a.d), s.hidden,
+                           s.intermediate, s.hidden, 2 * (size_t)persist_grid()};
+  size_t total = 0;
+  for (size_t w : words) total += align256(w * 8);
+  total += 256;  // error word
+  HIP_TRY(hipMalloc((void **)&m->pbuf, total));
+  HIP_TRY(hipMemsetAsync(m->pbuf, 0, total, m->stream));
+  m->pbuf_bytes = total;
+  uint64_t **dst[7] = {&a.tq, &a.tkv, &a.tpart, &a.txo, &a.th, &a.txd, &a.targ};
+  uint8_t *p = m->pbuf;
+  for (int i = 0; i < 7; i++) {
+    *dst[i] = (uint64_t *)p;
+    p += align256(words[i] * 8);
+  }
+  m->err = (uint32_t *)p;
+  a.err = m->err;
+  std::vector<PersistLayer> hl(s.num_layers);
+  for (size_t l = 0; l < s.num_layers; l++) {
+    const DevLayer &L = m->layers[l];
+    hl[l] = PersistLayer{L.ln1, L.wqkv, L.wo, L.ln2, L.wgu, L.wd, L.bqkv};
+  }
+  HIP_TRY(hipMalloc((void **)&m->dlayers, hl.size() * sizeof(PersistLayer)));
+  HIP_TRY(hipMemcpy(m->dlayers, hl.data(), hl.size() * sizeof(PersistLayer),
+                    hipMemcpyHostToDevice));
+  a.layers = m->dlayers;
+  a.embed = m->embed;
+  a.final_norm = m->final_norm;
+  a.head = m->head;
+  a.rope = m->rope;
+  a.kc = (float *)m->kc;
+  a.vc = (float *)m->vc;
+  a.layer_kv = m->layer_kv_elems;
+  a.logits = m->logits;
+  a.normed = m->normed;
+  a.x_out = m->x;
+  a.part_out = m->part;
+  a.part_cap = m->nparts;
+  a.part_in = m->part;
+  a.nparts_in = m->nparts;
+  a.state = m->state;
+  a.out_ids = m->out_ids;
+  m->persist_ok = true;
+  return MYOS_OK;
+}
+
+constexpr int kLaunchRefused = -1;
+
+bool use_persistent(const myos_model *m) {
+  return m->persist_ok && m->decode_mode != MYOS_DECODE_KERNELS;
+}
+
+// n greedy steps from the cursor in one cooperative launch; the error word
+// is checked after the stream synchronizes
+int persist_decode(myos_model *m, size_t n) {
+  const uint64_t tps = (uint64_t)persist_tags_per_step((int)m->s.num_layers);
+  if ((uint64_t)m->tag_base + n * tps >= 0xffffffffull) {
+    // the next tags would wrap: start again from zeroed words
+    HIP_TRY(hipMemsetAsync(m->pbuf, 0, m->pbuf_bytes, m->stream));
+    m->tag_base = 1;
+  }
+  PersistArgs a = m->pargs;
+  a.tag_base = m->tag_base;
+  a.steps = (uint32_t)n;
+  a.pos0 = (uint32_t)m->len;
+  if (m->trace_step >= 0 && (size_t)m->trace_step < n) {
+    a.trace = m->trace;
+    a.trace_step = (uint32_t)m->trace_step;
+  }
+  const hipError_t e = launch_decode_persistent(a, m->stream);
+  if (e == hipErrorCooperativeLaunchTooLarge || e == hipErrorInvalidConfiguration) {
+    (void)hipGetLastError();
+    return kLaunchRefused;  // nothing ran: the caller takes the per-kernel path
+  }
+  HIP_TRY(e);
+  m->tag_base += (uint32_t)(n * tps);
+  return MYOS_OK;
+}
+
+int persist_check_error(myos_model *m) {
+  uint32_t e = 0;
+  HIP_TRY(hipMemcpy(&e, m->err, 4, hipMemcpyDeviceToHost));
+  if (e) {
+    // a wait timed out: the run's ids and cache rows are not trustworthy
+    HIP_TRY(hipMemset(m->err, 0, 4));
+    return MYOS_E_HIP;
+  }
+  return MYOS_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -422,6 +545,9 @@ void myos_model_close(myos_model *m) {
   if (m->rope) (void)hipFree(m->rope);
   if (m->ws) (void)hipFree(m->ws);
   if (m->pf) (void)hipFree(m->pf);
+  if (m->pbuf) (void)hipFree(m->pbuf);
+  if (m->dlayers) (void)hipFree(m->dlayers);
+  if (m->trace) (void)hipFree(m->trace);
   if (m->host_state) (void)hipHostFree(m->host_state);
   if (m->stream) (void)hipStreamDestroy(m->stream);
   delete m;
@@ -641,6 +767,8 @@ static int open_impl(myos_model *m, const char *path, const myos_block_shape *sh
   HIP_TRY(hipMemcpyAsync(m->part, part0.data(), part0.size() * sizeof(float2),
                          hipMemcpyHostToDevice, m->stream));
   HIP_TRY(hipHostMalloc((void **)&m->host_state, 4 * sizeof(uint32_t), hipHostMallocDefault));
+  rc = setup_persistent(m);
+  if (rc) return rc;
   HIP_TRY(hipStreamSynchronize(m->stream));
   return MYOS_OK;
 }
@@ -792,14 +920,27 @@ int myos_greedy_decode(myos_model *m, size_t steps, uint32_t *out) {
   const size_t room = m->max_seq - m->len;
   const size_t n = steps < room ? steps : room;
   if (n) {
-    prepare_graph(m);  // capture (once) outside the timed region
+    bool persist = use_persistent(m);
+    if (!persist) prepare_graph(m);  // capture (once) outside the timed region
     int rc = write_state(m, (uint32_t)m->len, 0, 0, 0);
     if (rc) return rc;
     HIP_TRY(hipEventRecord(m->ev0, m->stream));
-    rc = run_steps(m, n);
+    rc = persist ? persist_decode(m, n) : run_steps(m, n);
+    if (rc == kLaunchRefused) {
+      // the device cannot hold the cooperative grid: per-kernel path from now on
+      m->persist_ok = false;
+      persist = false;
+      prepare_graph(m);
+      HIP_TRY(hipEventRecord(m->ev0, m->stream));
+      rc = run_steps(m, n);
+    }
     if (rc) return rc;
     HIP_TRY(hipEventRecord(m->ev1, m->stream));
     HIP_TRY(hipStreamSynchronize(m->stream));
+    if (persist) {
+      rc = persist_check_error(m);
+      if (rc) return rc;
+    }
     HIP_TRY(hipMemcpy(out, m->out_ids, n * 4, hipMemcpyDeviceToHost));
     float ms = 0;
     HIP_TRY(hipEventElapsedTime(&ms, m->ev0, m->ev1));
@@ -920,6 +1061,43 @@ int myos_kv_read(const myos_model *m, size_t layer, size_t head, size_t pos, flo
     }
   }
   return MYOS_OK;
+}
+
+int myos_set_decode_mode(myos_model *m, int mode) {
+  if (!m || mode < MYOS_DECODE_AUTO || mode > MYOS_DECODE_PERSISTENT) return MYOS_E_ARG;
+  if (mode == MYOS_DECODE_PERSISTENT && !m->persist_ok) return MYOS_E_SHAPE;
+  m->decode_mode = mode;
+  return MYOS_OK;
+}
+
+int myos_set_decode_trace(myos_model *m, int64_t step) {
+  if (!m) return MYOS_E_ARG;
+  if (step < 0) {
+    m->trace_step = -1;
+    return MYOS_OK;
+  }
+  if (!m->persist_ok) return MYOS_E_SHAPE;
+  if (!m->trace) {
+    const size_t n = (size_t)persist_grid() * (5 * m->s.num_layers + 3);
+    HIP_TRY(hipMalloc((void **)&m->trace, n * sizeof(uint64_t)));
+    HIP_TRY(hipMemset(m->trace, 0, n * sizeof(uint64_t)));
+  }
+  m->trace_step = step;
+  return MYOS_OK;
+}
+
+int myos_copy_decode_trace(const myos_model *m, uint64_t *out, size_t n) {
+  if (!m || !out) return MYOS_E_ARG;
+  if (!m->trace) return MYOS_E_SHAPE;
+  if (n != (size_t)persist_grid() * (5 * m->s.num_layers + 3)) return MYOS_E_SHAPE;
+  HIP_TRY(hipStreamSynchronize(m->stream));
+  HIP_TRY(hipMemcpy(out, m->trace, n * sizeof(uint64_t), hipMemcpyDeviceToHost));
+  return MYOS_OK;
+}
+
+int myos_decode_path(const myos_model *m) {
+  if (!m) return MYOS_E_ARG;
+  return use_persistent(m) ? MYOS_DECODE_PERSISTENT : MYOS_DECODE_KERNELS;
 }
 
 int myos_set_graph(myos_model *m, int enabled) {

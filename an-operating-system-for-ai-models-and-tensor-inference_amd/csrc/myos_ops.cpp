@@ -216,6 +216,7 @@ int myos_greedy_token(uint32_t *out, const float *logits, size_t n, myos_stream_
     a.part = part;
     a.nparts = parts;
     a.token_out = out;
+    a.vocab = (uint32_t)n;
     e = launch_argmax_final(a, s);
   }
   hipError_t f = hipFreeAsync(part, s);

@@ -103,6 +103,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernel-reps", type=int, default=20)
     ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument("--decode-path", choices=["auto", "kernels", "persistent"], default="auto")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: every box here has one MI355X and this build has "
@@ -126,6 +127,10 @@ def main():
     log(f"model resident in HBM in {t_load:.1f}s ({m.weight_bytes() / 1e9:.2f} GB weights)")
     if args.no_graph:
         m.set_graph(False)
+    m.set_decode_mode({"auto": myos.DECODE_AUTO, "kernels": myos.DECODE_KERNELS,
+                       "persistent": myos.DECODE_PERSISTENT}[args.decode_path])
+    path_name = "persistent" if m.decode_path() == myos.DECODE_PERSISTENT else "kernels"
+    log(f"decode path: {path_name}")
     rng = np.random.default_rng(2024)
     prompt = rng.integers(0, shape.vocab, args.prompt).astype(np.uint32)
 
@@ -207,7 +212,8 @@ def main():
                                f"{args.decode} greedy decode steps, batch 1",
                    "prompt_ids": args.prompt, "decode_steps": args.decode, "batch": 1,
                    "max_seq": max_seq, "kv_cache": args.kv, "accumulate": "f32",
-                   "graph": not args.no_graph, "parallelism": "single GPU"},
+                   "decode_path": path_name, "graph": not args.no_graph,
+                   "parallelism": "single GPU"},
         "prefill_tok_s": round(prefill_tok_s, 1),
         "decode_ms_per_token": round(td / (args.steps * args.decode) * 1e3, 4),
         "device_ms": {"prefill": round(dp / args.steps, 3), "decode": round(dd / args.steps, 3)},

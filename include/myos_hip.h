@@ -169,6 +169,28 @@ int myos_copy_normed(const myos_model *m, float *out, size_t n);
 int myos_kv_read(const myos_model *m, size_t layer, size_t head, size_t pos, float *k, float *v);
 /* 1 = capture each decode step in a hipGraph (default), 0 = plain launches. */
 int myos_set_graph(myos_model *m, int enabled);
+/* Decode path of myos_greedy_decode (no reference counterpart; the reference
+ * has one CPU path). PERSISTENT runs the whole call as one cooperative kernel
+ * whose workgroups hand activations to each other through tagged words;
+ * KERNELS replays per-step graphs of per-layer kernels; AUTO (default) takes
+ * PERSISTENT when the model allows it (f32 cache, hidden and q_dim <= 1536,
+ * intermediate <= 9216, head_dim <= 128 and a multiple of 8) and the device has
+ * >= 256 CUs with cooperative launch. Setting PERSISTENT where it is not
+ * available returns MYOS_E_SHAPE. myos_decode_path returns the path the next
+ * call takes. */
+enum { MYOS_DECODE_AUTO = 0, MYOS_DECODE_KERNELS = 1, MYOS_DECODE_PERSISTENT = 2 };
+int myos_set_decode_mode(myos_model *m, int mode);
+int myos_decode_path(const myos_model *m);
+/* Measurement hook for the persistent path (no reference counterpart): from
+ * the next greedy_decode on, decode step `step` of each call records, per
+ * workgroup, the device wall clock (100 MHz ticks) at 5 layers + 3 phase
+ * points: [0] token chosen; [1 + 5 l + p] layer l with p = 0 input ready,
+ * 1 attention items done, 2 attention merged, 3 o output ready, 4 h ready;
+ * [1 + 5 layers] head input ready; [2 + 5 layers] head done. step < 0 turns
+ * it off. myos_copy_decode_trace copies [grid][5 layers + 3] values, where
+ * grid is 256; n must equal that count. MYOS_E_SHAPE without the path. */
+int myos_set_decode_trace(myos_model *m, int64_t step);
+int myos_copy_decode_trace(const myos_model *m, uint64_t *out, size_t n);
 /* Device time of the last prefill / greedy_decode (hipEvent, milliseconds). */
 double myos_last_prefill_ms(const myos_model *m);
 double myos_last_decode_ms(const myos_model *m);

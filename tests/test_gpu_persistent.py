@@ -1,0 +1,157 @@
+"""Persistent greedy decode (one cooperative launch per greedy_decode call)
+against the oracle and against the per-kernel path.
+
+The persistent kernel computes the same step as forward_token
+(qwen25_block.rs:220-304) inside greedy_decode (qwen25_block.rs:765-780), with
+its own summation order, so it is held to the same rule as the per-kernel
+path: logits / hidden within max relative error 1e-2 and ids equal at every
+step where the oracle's top-1 / top-2 gap exceeds 1e-3 (after an allowed
+divergence at a smaller gap the trajectories separate and comparison stops).
+It also has to leave the decode state (cursor, cache rows, logits, argmax of
+the last logits) exactly where the per-kernel path expects it.
+"""
+import importlib
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+from model_fixtures import random_map, shape_dict, write_safetensors
+from parity import GAP, assert_logits_parity, max_rel, top2_gap
+
+myos = importlib.import_module("an-operating-system-for-ai-models-and-tensor-inference_amd")
+pytestmark = pytest.mark.gpu
+
+
+def to_block_shape(s):
+    return myos.make_shape(s["hidden"], s["num_q_heads"], s["num_kv_heads"], s["head_dim"],
+                           s["intermediate"], s["vocab"], s["num_layers"],
+                           rms_eps=float(s["rms_eps"]), rope_theta=float(s["rope_theta"]),
+                           tied_head=True)
+
+
+def oracle_steps(o, n):
+    """Greedy steps on the oracle, keeping each step's top-1 / top-2 gap."""
+    ids, gaps = [], []
+    for _ in range(n):
+        lg = o.logits()
+        tok = oracle.greedy_token(lg)
+        ids.append(int(tok))
+        gaps.append(top2_gap(lg))
+        assert o.forward_token(tok, o.cache_len()) == 0
+    return ids, gaps
+
+
+def agree(got, ref, gaps):
+    """Index of the first allowed divergence (len if none); fails on a real one."""
+    for i, (a, b) in enumerate(zip(got, ref)):
+        if a != b:
+            assert gaps[i] <= GAP, f"id {i}: {a} != {b} at top-2 gap {gaps[i]:.3e}"
+            return i
+    return len(ref)
+
+
+SMALL = [(256, 4, 2, 64, 512, 1000, 3), (128, 6, 1, 32, 384, 777, 2),
+         (384, 12, 2, 32, 1000, 4099, 2), (512, 4, 1, 128, 1536, 2048, 2)]
+
+
+@pytest.mark.parametrize("dims", SMALL)
+def test_persistent_small_models(tmp_path, dims):
+    s = shape_dict(*dims, 1e-6)
+    t = random_map(s, seed=sum(dims) + 1, std=0.05)
+    path = str(tmp_path / "m.safetensors")
+    write_safetensors(path, t)
+    max_seq = 80
+    g = myos.Model.open(path, to_block_shape(s), myos.KV_F32, max_seq)
+    if g.decode_path() != myos.DECODE_PERSISTENT:
+        g.close()
+        pytest.skip("the device cannot hold the cooperative decode grid")
+    k = myos.Model.open(path, to_block_shape(s), myos.KV_F32, max_seq)
+    k.set_decode_mode(myos.DECODE_KERNELS)
+    assert k.decode_path() == myos.DECODE_KERNELS
+    o = oracle.Model(s, t, max_seq, threads=4)
+    prompt = np.random.default_rng(11).integers(0, s["vocab"], 17)
+    for m in (g, k):
+        m.prefill(prompt)
+    assert o.prefill(prompt) == 0
+    # two launches: the second starts from the state the first left behind
+    ids_g = g.greedy_decode(20) + g.greedy_decode(23)
+    ids_k = k.greedy_decode(20) + k.greedy_decode(23)
+    ids_o, gaps = oracle_steps(o, 43)
+    n_ok = min(agree(ids_g, ids_o, gaps), agree(ids_k, ids_o, gaps))
+    assert g.cache_len() == k.cache_len() == 60
+    if n_ok == 43:
+        assert_logits_parity(g.logits(), o.logits(), "persistent, after 43 steps")
+        assert max_rel(g.hidden(), o.hidden()) < 1e-4
+        assert max_rel(g.normed(), o.normed()) < 1e-4
+        assert max_rel(g.logits(), k.logits()) < 1e-4
+        for layer in range(s["num_layers"]):
+            for pos in (0, 16, 17, 40, 59):
+                kg, vg = g.kv(layer, s["num_kv_heads"] - 1, pos)
+                ko, vo = o.kv(layer, s["num_kv_heads"] - 1, pos)
+                assert max_rel(kg, ko) < 1e-4 and max_rel(vg, vo) < 1e-4, (layer, pos)
+        # the per-kernel path continues from the persistent state
+        tok = oracle.greedy_token(o.logits())
+        g.forward_token(tok, 60)
+        assert o.forward_token(tok, 60) == 0
+        assert_logits_parity(g.logits(), o.logits(), "forward_token after persistent")
+        # ... and the persistent path from the per-kernel state
+        ids_o2, gaps2 = oracle_steps(o, 5)
+        agree(g.greedy_decode(5), ids_o2, gaps2)
+    g.close()
+    k.close()
+
+
+def test_persistent_until_cache_full(tmp_path):
+    s = shape_dict(256, 4, 2, 64, 512, 1000, 2, 1e-6)
+    t = random_map(s, seed=5, std=0.05)
+    path = str(tmp_path / "m.safetensors")
+    write_safetensors(path, t)
+    g = myos.Model.open(path, to_block_shape(s), myos.KV_F32, 12)
+    if g.decode_path() != myos.DECODE_PERSISTENT:
+        g.close()
+        pytest.skip("the device cannot hold the cooperative decode grid")
+    o = oracle.Model(s, t, 12, threads=2)
+    g.prefill([3, 1, 4])
+    assert o.prefill([3, 1, 4]) == 0
+    with pytest.raises(myos.MyosError) as e:
+        g.greedy_decode(20)
+    assert e.value.code == myos.E_KV_FULL
+    ids_o, gaps = oracle_steps(o, 9)
+    assert agree(e.value.partial, ids_o, gaps) >= 0
+    assert len(e.value.partial) == 9 and g.cache_len() == 12
+
+
+@pytest.fixture(scope="module")
+def qwen15(tmp_path_factory):
+    path = os.environ.get("MYOS_TEST_WEIGHTS_1_5B")
+    if not path:
+        path = str(tmp_path_factory.mktemp("w") / "qwen25_1_5b_seed0.safetensors")
+        myos.write_random_qwen25(path, myos.preset(myos.SHAPE_QWEN25_1_5B), seed=0, std=0.02)
+    s = shape_dict(1536, 12, 2, 128, 8960, 151936, 28, 1e-6)
+    return path, s, oracle.load_safetensors_bits(path)
+
+
+def test_persistent_qwen15_prefill128_greedy(qwen15):
+    """128 seeded prompt ids, then 12 greedy steps in one launch (seq 129..140,
+    five 32-position attention chunks per kv head)."""
+    path, s, t = qwen15
+    prompt = np.random.default_rng(2024).integers(0, 151936, 128)
+    g = myos.Model.open(path, myos.preset(myos.SHAPE_QWEN25_1_5B), myos.KV_F32, 256)
+    if g.decode_path() != myos.DECODE_PERSISTENT:
+        g.close()
+        pytest.skip("the device cannot hold the cooperative decode grid")
+    o = oracle.Model(s, t, 256, threads=16)
+    g.prefill(prompt)
+    assert o.prefill(prompt) == 0
+    ids_g = g.greedy_decode(12)
+    ids_o, gaps = oracle_steps(o, 12)
+    print("persistent ids", ids_g, "decode ms", g.last_decode_ms())
+    if agree(ids_g, ids_o, gaps) == 12:
+        assert_logits_parity(g.logits(), o.logits(), "after 12 persistent steps")
+        assert max_rel(g.hidden(), o.hidden()) < 1e-2
+        kg, vg = g.kv(27, 1, 139)
+        ko, vo = o.kv(27, 1, 139)
+        assert max_rel(kg, ko) < 1e-2 and max_rel(vg, vo) < 1e-2
+    g.close()
