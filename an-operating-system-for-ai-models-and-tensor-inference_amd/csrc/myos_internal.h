@@ -143,7 +143,7 @@ struct PersistArgs {
   float *kc, *vc;              // f32 cache base, layer stride = layer_kv
   size_t layer_kv;
   // tagged exchange buffers (zeroed once; tags only grow)
-  uint64_t *tq, *tkv, *tpart, *txo, *th, *txd, *targ;
+  uint64_t *tq, *tkv, *tpart, *tatt, *txo, *th, *txd, *targ;
   // outputs
   float *logits, *normed, *x_out;
   float2 *part_out;

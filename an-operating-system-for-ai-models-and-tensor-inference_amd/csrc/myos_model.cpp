@@ -410,8 +410,8 @@ int setup_persistent(myos_model *m) {
   a.qkv_rows = (int)m->qkv_rows;
   a.eps = s.rms_eps;
   if (m->kv_bf16 || !persist_device_ok(a)) return MYOS_OK;  // per-kernel path only
-  const size_t words[7] = {m->q_dim, 2 * m->kv_dim,
-                           persist_part_words(a.nq, a.max_seq, a.d), s.hidden,
+  const size_t words[8] = {m->q_dim, 2 * m->kv_dim,
+                           persist_part_words(a.nq, a.max_seq, a.d), m->q_dim, s.hidden,
                            s.intermediate, s.hidden, 2 * (size_t)persist_grid()};
   size_t total = 0;
   for (size_t w : words) total += align256(w * 8);
@@ -419,9 +419,9 @@ int setup_persistent(myos_model *m) {
   HIP_TRY(hipMalloc((void **)&m->pbuf, total));
   HIP_TRY(hipMemsetAsync(m->pbuf, 0, total, m->stream));
   m->pbuf_bytes = total;
-  uint64_t **dst[7] = {&a.tq, &a.tkv, &a.tpart, &a.txo, &a.th, &a.txd, &a.targ};
+  uint64_t **dst[8] = {&a.tq, &a.tkv, &a.tpart, &a.tatt, &a.txo, &a.th, &a.txd, &a.targ};
   uint8_t *p = m->pbuf;
-  for (int i = 0; i < 7; i++) {
+  for (int i = 0; i < 8; i++) {
     *dst[i] = (uint64_t *)p;
     p += align256(words[i] * 8);
   }

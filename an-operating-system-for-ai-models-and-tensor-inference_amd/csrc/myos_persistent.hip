@@ -35,7 +35,14 @@ constexpr int GPMAX = 5;             // gate/up row pairs per wavefront
 constexpr int AC = 32;               // attention positions per work item
 constexpr int HT = 2;                // head rows per tile
 constexpr int MAXH = 1536;           // hidden / q_dim limit of this kernel
+constexpr int MAXD = 128;            // head_dim limit
+constexpr int KV4 = (AC * MAXD / 4 + NT - 1) / NT;      // cached-row loads per thread
+constexpr int QW = (8 * MAXD + 2 * MAXD + NT - 1) / NT;  // q + k + v words per thread
 constexpr unsigned kSpinMax = 1u << 20;
+// A word's tag is its step's base + kTPL * layer + phase; the head's partials
+// take base + kTPL * layers; a step spans kTPL * layers + 2 tags.
+constexpr uint32_t kTPL = 6;
+constexpr uint32_t P_QKV = 0, P_PART = 1, P_XO = 2, P_H = 3, P_XD = 4, P_ATT = 5;
 constexpr size_t kMaxLds = 159 * 1024;  // dynamic LDS: 160 KB per workgroup on gfx950 less the static part
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -75,6 +82,14 @@ __device__ __forceinline__ bool err_raised(const PersistArgs &a) {
   return __hip_atomic_load(a.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u;
 }
 
+// Called every spin of a wait: every 64 spins, past the limit raise the error
+// word, and report whether it is raised (then every wait gives up at once).
+__device__ __forceinline__ bool spin_fail(const PersistArgs &a, unsigned spins) {
+  if ((spins & 63) != 63) return false;
+  if (spins > kSpinMax) __hip_atomic_store(a.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return err_raised(a);
+}
+
 // Gather n tagged words (index i -> src[map(i)]) into dst[i]; the whole
 // workgroup waits until every word carries `tag`. Returns false (and leaves
 // garbage in dst) when the wait failed or an earlier one did.
@@ -94,12 +109,9 @@ __device__ bool tgather(const uint64_t *src, Map map, int n, uint32_t tag, float
 #pragma unroll
       for (int u = 0; u < U; u++) ready = ready && (uint32_t)(w[u] >> 32) == tag;
       if (ready) break;
-      if ((spins & 63) == 63) {
-        if (spins > kSpinMax) __hip_atomic_store(a.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (err_raised(a)) {
-          ok = false;
-          break;
-        }
+      if (spin_fail(a, spins)) {
+        ok = false;
+        break;
       }
       __builtin_amdgcn_s_sleep(1);
     }
@@ -143,12 +155,9 @@ __device__ bool tgather_lin(const uint64_t *src, int n, uint32_t tag, float *dst
 #pragma unroll
       for (int u = 0; u < U; u++) ready = ready && (uint32_t)(w[u] >> 32) == tag;
       if (ready) break;
-      if ((spins & 63) == 63) {
-        if (spins > kSpinMax) __hip_atomic_store(a.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (err_raised(a)) {
-          ok = false;
-          break;
-        }
+      if (spin_fail(a, spins)) {
+        ok = false;
+        break;
       }
       __builtin_amdgcn_s_sleep(1);
     }
@@ -280,7 +289,7 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int H = a.H, I = a.I, d = a.d, half = d >> 1, gq = a.nq / a.nkv;
   const int qdim = a.nq * d, kvdim = a.nkv * d;
-  const uint32_t TPS = (uint32_t)(a.L * 5 + 2);
+  const uint32_t TPS = (uint32_t)a.L * kTPL + 2;
   const int nchmax = (a.max_seq + AC - 1) / AC;
   // ownership
   const int qper = (((a.qkv_rows + NB - 1) / NB) + 1) & ~1;
@@ -332,7 +341,7 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
         }
       } else {
         float *pp = big;  // [2 * NB]: value, index bits
-        tgather_lin<1>(a.targ, 2 * NB, tstep - TPS + (uint32_t)a.L * 5, pp, a, &fail_s);
+        tgather_lin<1>(a.targ, 2 * NB, tstep - TPS + (uint32_t)a.L * kTPL, pp, a, &fail_s);
         if (tid < NB) {
           bv = pp[2 * tid];
           bi = __float_as_uint(pp[2 * tid + 1]);
@@ -368,11 +377,11 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
 
     for (int l = 0; l < a.L; l++) {
       const PersistLayer &L = a.layers[l];
-      const uint32_t T = tstep + (uint32_t)l * 5;
+      const uint32_t T = tstep + (uint32_t)l * kTPL;
       float *kc = a.kc + (size_t)l * a.layer_kv, *vc = a.vc + (size_t)l * a.layer_kv;
 
-      // ---- QKV + bias + RoPE + KV store (tag T) ----------------------------
-      if (l > 0) tgather_lin<3>(a.txd, H, T - 1, xs, a, &fail_s);
+      // ---- QKV + bias + RoPE + KV store (tag T + P_QKV) ---------------------
+      if (l > 0) tgather_lin<3>(a.txd, H, T - kTPL + P_XD, xs, a, &fail_s);
       mark(a, s, 1 + 5 * l);
       rmsnorm_lds(xs, L.ln1, H, a.eps, red);
       if (has_q) {
@@ -386,22 +395,22 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
             const float2 cs = a.rope[(size_t)pos * half + p];
             const float o0 = b0 * cs.x - b1 * cs.y, o1 = b1 * cs.x + b0 * cs.y;
             if (is_q) {
-              tput(a.tq + head * d + p, o0, T);
-              tput(a.tq + head * d + p + half, o1, T);
+              tput(a.tq + head * d + p, o0, T + P_QKV);
+              tput(a.tq + head * d + p + half, o1, T + P_QKV);
             } else {
               const size_t base = ((size_t)head * a.max_seq + pos) * d;
               cstore(kc + base + p, o0);
               cstore(kc + base + p + half, o1);
-              tput(a.tkv + head * d + p, o0, T);
-              tput(a.tkv + head * d + p + half, o1, T);
+              tput(a.tkv + head * d + p, o0, T + P_QKV);
+              tput(a.tkv + head * d + p + half, o1, T + P_QKV);
             }
           } else {
             const int rr = qrow - qdim - kvdim, head = rr / d, j = rr - head * d;
             const size_t base = ((size_t)head * a.max_seq + pos) * d + j;
             cstore(vc + base, b0);
             cstore(vc + base + 1, b1);
-            tput(a.tkv + kvdim + head * d + j, b0, T);
-            tput(a.tkv + kvdim + head * d + j + 1, b1, T);
+            tput(a.tkv + kvdim + head * d + j, b0, T + P_QKV);
+            tput(a.tkv + kvdim + head * d + j + 1, b1, T + P_QKV);
           }
           // the cache rows must be complete before anything this workgroup
           // publishes later: later steps read them without tags
@@ -409,51 +418,84 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
         }
       }
 
-      // ---- attention partials for (kv head, chunk) items (tag T + 1) --------
+      // ---- attention partials for (kv head, chunk) items (tag T + P_PART) ----
       const int nch = (seq + AC - 1) / AC;
       for (int it = wg; it < a.nkv * nch; it += NB) {
         const int g = it % a.nkv, c = it / a.nkv;
         const int t0 = c * AC, n = min(AC, seq - t0);
+        const bool has_cur = (int)pos < t0 + n;  // this step's row ends the chunk
+        const int nold = has_cur ? n - 1 : n;
         float *q_s = big;                    // [gq][d]
         float *k_s = q_s + gq * d;           // [AC][d + 1]
         float *v_s = k_s + AC * (d + 1);     // [AC][d]
         float *p_s = v_s + AC * d;           // [gq][AC]
         float *ml = p_s + gq * AC;           // [gq][2]
-        float *cur = ml + 2 * gq;            // [2][d] this step's k, v of head g
-        const int qoff = g * gq * d;
-        tgather<2>(a.tq, [qoff](int i) { return qoff + i; }, gq * d, T, q_s, a, &fail_s);
-        const bool has_cur = (int)pos < t0 + n;
-        if (has_cur) {
-          const int goff = g * d;
-          tgather<1>(a.tkv, [goff, kvdim, d](int i) { return i < d ? goff + i : kvdim + goff + i - d; },
-                     2 * d, T, cur, a, &fail_s);
-        }
-        // cached rows (positions < pos) with device-coherent 16-byte loads
-        const int nold = has_cur ? n - 1 : n;
+        // cached rows (positions < pos, complete before this step) and the
+        // tagged q heads + this step's k, v of head g, all in one round trip
         const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
             kc, (short)0, (int)(a.layer_kv * sizeof(float)), 0x00020000);
         const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
             vc, (short)0, (int)(a.layer_kv * sizeof(float)), 0x00020000);
         const int dq = d >> 2;
-        for (int i = tid; i < nold * dq; i += NT) {
-          const int t = i / dq, j4 = i - t * dq;
-          const uint32_t off = (uint32_t)((((size_t)g * a.max_seq + t0 + t) * d + j4 * 4) * 4);
-          const u32x4 kv = __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 16);
-          const u32x4 vv = __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, 16);
-          float *kd = k_s + t * (d + 1) + j4 * 4;
-          kd[0] = __uint_as_float(kv.x);
-          kd[1] = __uint_as_float(kv.y);
-          kd[2] = __uint_as_float(kv.z);
-          kd[3] = __uint_as_float(kv.w);
-          *(float4 *)(v_s + t * d + j4 * 4) =
-              make_float4(__uint_as_float(vv.x), __uint_as_float(vv.y), __uint_as_float(vv.z),
-                          __uint_as_float(vv.w));
-        }
-        if (has_cur)
-          for (int j = tid; j < d; j += NT) {
-            k_s[nold * (d + 1) + j] = cur[j];
-            v_s[nold * d + j] = cur[d + j];
+        u32x4 kr[KV4], vr[KV4];
+#pragma unroll
+        for (int u = 0; u < KV4; u++) {
+          const int i = tid + u * NT;
+          if (i < nold * dq) {
+            const int t = i / dq, j4 = i - t * dq;
+            const uint32_t off = (uint32_t)((((size_t)g * a.max_seq + t0 + t) * d + j4 * 4) * 4);
+            kr[u] = __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 16);
+            vr[u] = __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, 16);
           }
+        }
+        const int nqw = gq * d, nw = nqw + (has_cur ? 2 * d : 0);
+        const uint64_t *srcw[QW];
+#pragma unroll
+        for (int u = 0; u < QW; u++) {
+          const int i = tid + u * NT, r = i - nqw;
+          srcw[u] = i < nqw ? a.tq + g * gq * d + i
+                            : r < d ? a.tkv + g * d + r : a.tkv + kvdim + g * d + (r - d);
+        }
+        uint64_t w[QW];
+        for (unsigned spins = 0; fail_s == 0; spins++) {
+          bool ready = true;
+#pragma unroll
+          for (int u = 0; u < QW; u++) {
+            w[u] = tid + u * NT < nw ? tload(srcw[u]) : ((uint64_t)(T + P_QKV) << 32);
+            ready = ready && (uint32_t)(w[u] >> 32) == T + P_QKV;
+          }
+          if (ready) break;
+          if (spin_fail(a, spins)) {
+            fail_s = 1;
+            break;
+          }
+          __builtin_amdgcn_s_sleep(1);
+        }
+#pragma unroll
+        for (int u = 0; u < KV4; u++) {
+          const int i = tid + u * NT;
+          if (i < nold * dq) {
+            const int t = i / dq, j4 = i - t * dq;
+            float *kd = k_s + t * (d + 1) + j4 * 4;
+            kd[0] = __uint_as_float(kr[u].x);
+            kd[1] = __uint_as_float(kr[u].y);
+            kd[2] = __uint_as_float(kr[u].z);
+            kd[3] = __uint_as_float(kr[u].w);
+            *(float4 *)(v_s + t * d + j4 * 4) =
+                make_float4(__uint_as_float(vr[u].x), __uint_as_float(vr[u].y),
+                            __uint_as_float(vr[u].z), __uint_as_float(vr[u].w));
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < QW; u++) {
+          const int i = tid + u * NT, r = i - nqw;
+          const float v = __uint_as_float((uint32_t)w[u]);
+          if (i < nqw) q_s[i] = v;
+          else if (i < nw) {
+            if (r < d) k_s[nold * (d + 1) + r] = v;
+            else v_s[nold * d + r - d] = v;
+          }
+        }
         __syncthreads();
         const float scale = 1.0f / sqrtf((float)d);
         for (int i = tid; i < gq * n; i += NT) {
@@ -486,112 +528,65 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
           float o = 0.f;
           for (int t = 0; t < n; t++) o = fmaf(p_s[h * AC + t], v_s[t * d + j], o);
           uint64_t *dst = a.tpart + ((size_t)(g * gq + h) * nchmax + c) * (d + 2);
-          tput(dst + j, o, T + 1);
+          tput(dst + j, o, T + P_PART);
           if (j == 0) {
-            tput(dst + d, ml[2 * h], T + 1);
-            tput(dst + d + 1, ml[2 * h + 1], T + 1);
+            tput(dst + d, ml[2 * h], T + P_PART);
+            tput(dst + d + 1, ml[2 * h + 1], T + P_PART);
           }
         }
         __syncthreads();
       }
 
-      mark(a, s, 2 + 5 * l);
-      // ---- o projection: merge chunks, residual (tag T + 2) ------------------
-      {
-        float *ms = big, *ls = big + a.nq * nch;
-        const int nv = nch, dd = d + 2;
-        tgather<2>(a.tpart,
-                   [nv, nchmax, dd, d](int i) {
-                     const int h = i / (2 * nv), r = i - h * 2 * nv;
-                     return (h * nchmax + (r >> 1)) * dd + d + (r & 1);
-                   },
-                   2 * a.nq * nv, T + 1, ms + a.nq * nv * 2 /* temp */, a, &fail_s);
-        // unpack (m, l) pairs, then per head weights w_c = e^(m_c - M) / sum
-        float *tmp = ms + a.nq * nv * 2;
-        for (int i = tid; i < a.nq * nv; i += NT) {
-          ms[i] = tmp[2 * i];
-          ls[i] = tmp[2 * i + 1];
-        }
-        __syncthreads();
-        for (int h = tid; h < a.nq; h += NT) {
+      // ---- merge: q head h's chunks -> att[h] (tag T + P_ATT), on the last
+      // workgroups (attention items start at the first) --------------------
+      const int mh = NB - 1 - wg;
+      if (mh < a.nq) {
+        const int dd = d + 2;
+        float *pc = big;                     // [nch][d + 2] gathered partials
+        float *wc = big + nch * dd;          // [nch] chunk weights
+        const int base = mh * nchmax * dd;
+        tgather<2>(a.tpart, [base](int i) { return base + i; }, nch * dd, T + P_PART, pc, a, &fail_s);
+        if (tid == 0) {
+          // w_c = e^(m_c - M) / sum_c e^(m_c - M) l_c
           float mx = -INFINITY;
-          for (int c = 0; c < nv; c++) mx = fmaxf(mx, ms[h * nv + c]);
+          for (int c = 0; c < nch; c++) mx = fmaxf(mx, pc[c * dd + d]);
           float lsum = 0.f;
-          for (int c = 0; c < nv; c++) {
-            const float w = expf(ms[h * nv + c] - mx);
-            ms[h * nv + c] = w;
-            lsum = fmaf(w, ls[h * nv + c], lsum);
+          for (int c = 0; c < nch; c++) {
+            const float e = expf(pc[c * dd + d] - mx);
+            wc[c] = e;
+            lsum = fmaf(e, pc[c * dd + d + 1], lsum);
           }
           const float inv = 1.0f / lsum;
-          for (int c = 0; c < nv; c++) ms[h * nv + c] *= inv;
+          for (int c = 0; c < nch; c++) wc[c] *= inv;
         }
         __syncthreads();
-        // att[i] = sum_c w[h][c] o_c[h][j]: up to 3 outputs x 4 chunks per batch
-        constexpr int R = (MAXH + NT - 1) / NT, CB = 4;
-        float acc[R];
-#pragma unroll
-        for (int r = 0; r < R; r++) acc[r] = 0.f;
-        for (int c0 = 0; c0 < nv && fail_s == 0; c0 += CB) {
-          uint64_t w[R][CB];
-          for (unsigned spins = 0;; spins++) {
-            bool ready = true;
-#pragma unroll
-            for (int r = 0; r < R; r++)
-#pragma unroll
-              for (int u = 0; u < CB; u++) {
-                const int i = tid + r * NT, c = c0 + u;
-                if (i < qdim && c < nv) {
-                  const int h = i / d, j = i - h * d;
-                  w[r][u] = tload(a.tpart + ((size_t)h * nchmax + c) * dd + j);
-                } else {
-                  w[r][u] = (uint64_t)(T + 1) << 32;
-                }
-              }
-#pragma unroll
-            for (int r = 0; r < R; r++)
-#pragma unroll
-              for (int u = 0; u < CB; u++) ready = ready && (uint32_t)(w[r][u] >> 32) == T + 1;
-            if (ready) break;
-            if ((spins & 63) == 63) {
-              if (spins > kSpinMax)
-                __hip_atomic_store(a.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-              if (err_raised(a)) {
-                fail_s = 1;
-                break;
-              }
-            }
-            __builtin_amdgcn_s_sleep(1);
-          }
-#pragma unroll
-          for (int r = 0; r < R; r++)
-#pragma unroll
-            for (int u = 0; u < CB; u++) {
-              const int i = tid + r * NT, c = c0 + u;
-              if (i < qdim && c < nv)
-                acc[r] = fmaf(ms[(i / d) * nv + c], __uint_as_float((uint32_t)w[r][u]), acc[r]);
-            }
+        for (int j = tid; j < d; j += NT) {
+          float acc = 0.f;
+          for (int c = 0; c < nch; c++) acc = fmaf(wc[c], pc[c * dd + j], acc);
+          tput(a.tatt + mh * d + j, acc, T + P_ATT);
         }
-#pragma unroll
-        for (int r = 0; r < R; r++)
-          if (tid + r * NT < qdim) att[tid + r * NT] = acc[r];
         __syncthreads();
-        mark(a, s, 3 + 5 * l);
-        if (has_x) {
-          const float y = dotrow<HC>(wo, att, qdim, lane);
-          if (lane == 0) {
-            xl[wave] += y;
-            tput(a.txo + xrow, xl[wave], T + 2);
-          }
+      }
+      mark(a, s, 2 + 5 * l);
+
+      // ---- o projection + residual (tag T + P_XO) -----------------------------
+      tgather_lin<3>(a.tatt, qdim, T + P_ATT, att, a, &fail_s);
+      mark(a, s, 3 + 5 * l);
+      if (has_x) {
+        const float y = dotrow<HC>(wo, att, qdim, lane);
+        if (lane == 0) {
+          xl[wave] += y;
+          tput(a.txo + xrow, xl[wave], T + P_XO);
         }
       }
 
-      // ---- gate/up + SwiGLU (tag T + 3) --------------------------------------
+      // ---- gate/up + SwiGLU (tag T + P_H) -------------------------------------
       // pairs 0 and 1 load while X_o is awaited; pair p + 2 loads while p computes
       ldrow<HC>(gA0, L.wgu, H, gu_row(0), gu_row(0) < g1, lane);
       ldrow<HC>(gA1, L.wgu, H, gu_row(0) + 1, gu_row(0) < g1, lane);
       ldrow<HC>(gB0, L.wgu, H, gu_row(1), gu_row(1) < g1, lane);
       ldrow<HC>(gB1, L.wgu, H, gu_row(1) + 1, gu_row(1) < g1, lane);
-      tgather_lin<3>(a.txo, H, T + 2, xs, a, &fail_s);
+      tgather_lin<3>(a.txo, H, T + P_XO, xs, a, &fail_s);
       mark(a, s, 4 + 5 * l);
       rmsnorm_lds(xs, L.ln2, H, a.eps, red);
 #pragma unroll
@@ -614,28 +609,28 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
           ldrow<HC>(gB0, L.wgu, H, nrow, nv2, lane);
           ldrow<HC>(gB1, L.wgu, H, nrow + 1, nv2, lane);
         }
-        if (row < g1 && lane == 0) tput(a.th + (row >> 1), silu(y0) * y1, T + 3);
+        if (row < g1 && lane == 0) tput(a.th + (row >> 1), silu(y0) * y1, T + P_H);
       }
       // next weights: down of this layer, QKV and o of the next layer
       uint8_t *wd_s = wdl + (size_t)wave * I * 2;
       dma_row(L.wd, I, xrow, has_x, wd_s, lane);
       if (l + 1 < a.L) issue_qo(l + 1);
 
-      // ---- down + residual (tag T + 4) -----------------------------------------
-      tgather_lin<18>(a.th, I, T + 3, big, a, &fail_s);
+      // ---- down + residual (tag T + P_XD) -------------------------------------
+      tgather_lin<18>(a.th, I, T + P_H, big, a, &fail_s);
       mark(a, s, 5 + 5 * l);
       if (has_x) {
         const float y = dotrow_lds(wd_s, big, I, lane);
         if (lane == 0) {
           xl[wave] += y;
-          tput(a.txd + xrow, xl[wave], T + 4);
+          tput(a.txd + xrow, xl[wave], T + P_XD);
         }
       }
     }
 
     // ---- final norm + head + argmax partial (tag tstep + 5L) -----------------
-    const uint32_t TH = tstep + (uint32_t)a.L * 5;
-    tgather_lin<3>(a.txd, H, TH - 1, xs, a, &fail_s);
+    const uint32_t TH = tstep + (uint32_t)a.L * kTPL;
+    tgather_lin<3>(a.txd, H, TH - kTPL + P_XD, xs, a, &fail_s);
     mark(a, s, 1 + 5 * a.L);
     rmsnorm_lds(xs, a.final_norm, H, a.eps, red);
     if (wg == 0)
@@ -696,7 +691,7 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
   // ---- hand the state back to the per-kernel path ---------------------------
   if (tid < NW && x0 + tid < x1) a.x_out[x0 + tid] = xl[tid];
   if (wg == 0) {
-    const uint32_t TH = a.tag_base + (a.steps - 1) * TPS + (uint32_t)a.L * 5;
+    const uint32_t TH = a.tag_base + (a.steps - 1) * TPS + (uint32_t)a.L * kTPL;
     float *pp = big;
     tgather_lin<1>(a.targ, 2 * NB, TH, pp, a, &fail_s);
     float bv = -INFINITY;
@@ -735,7 +730,7 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
 }  // namespace
 
 int persist_grid() { return NB; }
-int persist_tags_per_step(int layers) { return layers * 5 + 2; }
+int persist_tags_per_step(int layers) { return layers * (int)kTPL + 2; }
 size_t persist_part_words(int nq, int max_seq, int d) {
   return (size_t)nq * ((max_seq + AC - 1) / AC) * (size_t)(d + 2);
 }
@@ -743,7 +738,7 @@ size_t persist_part_words(int nq, int max_seq, int d) {
 bool persist_supported(int H, int I, int qdim, int d, int gq) {
   if (H % 8 || I % 8 || qdim % 8) return false;
   if (H > MAXH || qdim > MAXH || I > MAXI) return false;
-  if (d % 8 || d > 128 || gq > 8) return false;
+  if (d % 8 || d > MAXD || gq > 8) return false;
   // each workgroup's gate/up pairs fit GPMAX per wavefront, residual rows and
   // QKV pairs one per wavefront
   const int gper = (((2 * I + NB - 1) / NB) + 1) & ~1;
@@ -759,7 +754,8 @@ bool persist_supported(int H, int I, int qdim, int d, int gq) {
 static size_t persist_lds(PersistArgs &a) {
   const int gq = a.nq / a.nkv;
   const size_t attn = (size_t)gq * a.d + AC * (a.d + 1) + AC * a.d + gq * AC + 2 * gq + 2 * a.d;
-  const size_t merge = 4 * (size_t)a.nq * ((a.max_seq + AC - 1) / AC);
+  const size_t nchm = (size_t)(a.max_seq + AC - 1) / AC;
+  const size_t merge = nchm * (a.d + 2) + nchm;
   size_t big = (size_t)a.I;
   if (attn > big) big = attn;
   if (merge > big) big = merge;
