@@ -33,16 +33,44 @@ __device__ __forceinline__ uint16_t f2bf(float f) {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
+// Cross-lane reductions with DPP lane moves (a few cycles each; a
+// __shfl_xor is an LDS permute round trip). gfx9 DPP controls: quad_perm
+// [1,0,3,2] = 0xB1, [2,3,0,1] = 0x4E, row_half_mirror 0x141, row_mirror
+// 0x140, row_bcast:15 0x142, row_bcast:31 0x143. Rows outside ROW_MASK keep
+// `old`, the identity of the reduction.
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ float dpp(float v, float old) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(old), __float_as_int(v), CTRL,
+                                                    ROW_MASK, 0xF, false));
+}
+// sum / max over aligned groups of W lanes (W = 2, 4, 8, 16 or the whole
+// 64-lane wavefront); every lane of a group gets the result
 template <int W>
 __device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-  for (int o = W / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, W);
+  static_assert(W == 2 || W == 4 || W == 8 || W == 16 || W == 64, "group width");
+  if (W >= 2) v += dpp<0xB1>(v, 0.f);
+  if (W >= 4) v += dpp<0x4E>(v, 0.f);
+  if (W >= 8) v += dpp<0x141>(v, 0.f);
+  if (W >= 16) v += dpp<0x140>(v, 0.f);
+  if (W == 64) {
+    v += dpp<0x142, 0xA>(v, 0.f);  // row 0 into row 1, row 2 into row 3
+    v += dpp<0x143, 0xC>(v, 0.f);  // rows 0 + 1 into rows 2, 3: lane 63 holds the total
+    v = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+  }
   return v;
 }
 template <int W>
 __device__ __forceinline__ float group_max(float v) {
-#pragma unroll
-  for (int o = W / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, W));
+  static_assert(W == 2 || W == 4 || W == 8 || W == 16 || W == 64, "group width");
+  if (W >= 2) v = fmaxf(v, dpp<0xB1>(v, -INFINITY));
+  if (W >= 4) v = fmaxf(v, dpp<0x4E>(v, -INFINITY));
+  if (W >= 8) v = fmaxf(v, dpp<0x141>(v, -INFINITY));
+  if (W >= 16) v = fmaxf(v, dpp<0x140>(v, -INFINITY));
+  if (W == 64) {
+    v = fmaxf(v, dpp<0x142, 0xA>(v, -INFINITY));
+    v = fmaxf(v, dpp<0x143, 0xC>(v, -INFINITY));
+    v = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+  }
   return v;
 }
 

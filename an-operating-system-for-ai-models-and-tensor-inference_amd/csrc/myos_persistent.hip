@@ -52,15 +52,34 @@ __device__ __forceinline__ float bf_lo(uint32_t v) { return __uint_as_float(v <<
 __device__ __forceinline__ float bf_hi(uint32_t v) { return __uint_as_float(v & 0xffff0000u); }
 __device__ __forceinline__ float bf16f(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
 
+// Cross-lane reductions with DPP lane moves (a few cycles each; a
+// __shfl_xor is an LDS permute round trip). gfx9 DPP controls: quad_perm
+// [1,0,3,2] = 0xB1, [2,3,0,1] = 0x4E, row_half_mirror 0x141, row_mirror
+// 0x140, row_bcast:15 0x142, row_bcast:31 0x143. Rows outside ROW_MASK keep
+// `old`, the identity of the reduction.
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ float dpp(float v, float old) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(old), __float_as_int(v), CTRL,
+                                                    ROW_MASK, 0xF, false));
+}
+// sum / max over the wavefront, returned to every lane
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
+  v += dpp<0xB1>(v, 0.f);
+  v += dpp<0x4E>(v, 0.f);
+  v += dpp<0x141>(v, 0.f);
+  v += dpp<0x140>(v, 0.f);
+  v += dpp<0x142, 0xA>(v, 0.f);  // row 0 into row 1, row 2 into row 3
+  v += dpp<0x143, 0xC>(v, 0.f);  // rows 0 + 1 into rows 2, 3: lane 63 holds the total
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  return v;
+  v = fmaxf(v, dpp<0xB1>(v, -INFINITY));
+  v = fmaxf(v, dpp<0x4E>(v, -INFINITY));
+  v = fmaxf(v, dpp<0x141>(v, -INFINITY));
+  v = fmaxf(v, dpp<0x140>(v, -INFINITY));
+  v = fmaxf(v, dpp<0x142, 0xA>(v, -INFINITY));
+  v = fmaxf(v, dpp<0x143, 0xC>(v, -INFINITY));
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
 __device__ __forceinline__ bool beats(float v, uint32_t i, float bv, uint32_t bi) {

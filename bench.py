@@ -58,6 +58,51 @@ def kv_bytes_per_token(s, seq, kv_bytes) -> int:
     return s.num_layers * 2 * s.num_kv_heads * s.head_dim * seq * kv_bytes
 
 
+def gemv_microbench(reps=5):
+    """Isolated op-tier GEMV (bf16 W, f32 x, f32 accumulate) at the five
+    decode shapes. One hipGraph per shape launches the GEMV once per weight
+    copy; the copies total >= 512 MB (twice the last-level cache), so replays
+    stream HBM. avg_us = replay time / launches (inter-kernel gaps included),
+    from events on the replay stream."""
+    import torch
+    out = {}
+    shapes = {"lm_head": (151936, 1536), "gate_or_up": (8960, 1536), "down": (1536, 8960),
+              "q_or_o": (1536, 1536), "k_or_v": (256, 1536)}
+    for name, (m, k) in shapes.items():
+        nbytes = m * k * 2
+        copies = max(2, -(-(512 << 20) // nbytes))
+        gen = torch.Generator(device="cuda").manual_seed(m + k)
+        ws = [(torch.randn(m, k, device="cuda", generator=gen) * 0.02).to(torch.bfloat16)
+              for _ in range(copies)]
+        x = torch.randn(k, device="cuda", generator=gen)
+        y = torch.empty(m, device="cuda")
+        side = torch.cuda.Stream()
+        with torch.cuda.stream(side):
+            for w in ws:
+                myos.gemv_bf16(y, w, x, m, k)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for w in ws:
+                myos.gemv_bf16(y, w, x, m, k)
+        graph.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            graph.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / (reps * len(ws))
+        by = nbytes + k * 4 + m * 4
+        out[name] = {"m": m, "k": k, "avg_us": round(us, 2), "GBps": round(by / us / 1e3, 1),
+                     "frac_hbm": round(by / us / 1e3 / (HBM_PEAK / 1e9), 4),
+                     "weight_copies": len(ws)}
+        del graph, ws
+        torch.cuda.empty_cache()
+    return out
+
+
 def cpu_baseline(path, shape, prompt, n_steps, gpu_ids):
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle
@@ -104,12 +149,18 @@ def main():
     ap.add_argument("--kernel-reps", type=int, default=20)
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--decode-path", choices=["auto", "kernels", "persistent"], default="auto")
+    ap.add_argument("--no-gemv-microbench", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: every box here has one MI355X and this build has "
               f"no multi-GPU path (--gpus {args.gpus} requested)", file=sys.stderr)
         sys.exit(2)
 
+    if not args.no_gemv_microbench:
+        # torch carries its own HIP runtime: it must initialise the device before
+        # the library's runtime does (the microbench allocates through torch)
+        import torch
+        torch.cuda.init()
     shape = myos.preset(myos.SHAPE_QWEN25_1_5B)
     path = args.weights or "/tmp/myos_bench/qwen25_1_5b_seed0.safetensors"
     if not os.path.exists(path):
@@ -188,6 +239,11 @@ def main():
                 "algorithmic_bytes": dom["bytes"]}
     m.close()
 
+    micro = None if args.no_gemv_microbench else gemv_microbench()
+    if micro:
+        log("gemv microbench: " + ", ".join(f"{n} {v['avg_us']}us {v['GBps']}GB/s"
+                                             for n, v in micro.items()))
+
     cpu = None
     if not args.no_cpu_baseline:
         n = args.cpu_decode_steps
@@ -220,7 +276,8 @@ def main():
         "decode_roofline": {"bytes_per_token": int(b_tok), "achieved_GBps":
                             round(decode_tok_s * b_tok / 1e9, 1), "peak_GBps": HBM_PEAK / 1e9,
                             "frac": round(decode_frac, 4)},
-        "roofline": roofline, "kernels": kernels, "t_load_s": round(t_load, 2),
+        "roofline": roofline, "kernels": kernels, "gemv_microbench": micro,
+        "t_load_s": round(t_load, 2),
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
