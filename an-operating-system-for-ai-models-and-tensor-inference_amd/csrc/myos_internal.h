@@ -133,6 +133,7 @@ hipError_t launch_permute_rows(uint16_t *dst, const uint16_t *src, const int *pe
 struct PersistLayer {
   const uint16_t *ln1, *wqkv, *wo, *ln2, *wgu, *wd;
   const float *bqkv;
+  const uint16_t *wdT;         // down transposed [I][H] (streamed kernel only)
 };
 struct PersistArgs {
   int H, I, V, L, nq, nkv, d, max_seq, qkv_rows;
@@ -144,6 +145,8 @@ struct PersistArgs {
   size_t layer_kv;
   // tagged exchange buffers (zeroed once; tags only grow)
   uint64_t *tq, *tkv, *tpart, *tatt, *txo, *th, *txd, *targ;
+  uint64_t *tpd;               // streamed kernel: [grid][H] down partials per workgroup
+  int ring_slots;              // streamed kernel: set by the launcher
   // outputs
   float *logits, *normed, *x_out;
   float2 *part_out;
@@ -163,6 +166,19 @@ size_t persist_part_words(int nq, int max_seq, int d);
 bool persist_supported(int H, int I, int qdim, int d, int gq);
 bool persist_device_ok(const PersistArgs &a);  // shape, LDS and the current device fit
 hipError_t launch_decode_persistent(const PersistArgs &a, hipStream_t s);
+
+// ---- streamed persistent decode (myos_stream.hip) -----------------------------
+// The same contract as launch_decode_persistent; every workgroup keeps its
+// weight rows streaming from HBM across the dependency chain. Needs
+// PersistLayer::wdT and PersistArgs::tpd.
+bool stream_supported(int H, int I, int V, int qdim, int d, int gq, int nkv, int max_seq,
+                      int qkv_rows);
+bool stream_device_ok(const PersistArgs &a);
+hipError_t launch_decode_stream(const PersistArgs &a, hipStream_t s);
+size_t stream_tpd_words(int H);  // words of the down-partial buffer
+size_t stream_part_words(int nq, int max_seq, int d);  // attention partial words
+hipError_t launch_transpose_bf16(uint16_t *dst, const uint16_t *src, int rows, int cols,
+                                 hipStream_t s);
 
 const char *kernel_build_info();
 

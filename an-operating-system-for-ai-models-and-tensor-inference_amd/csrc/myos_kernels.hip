@@ -930,6 +930,23 @@ __global__ void permute_rows_kernel(uint16_t *dst, const uint16_t *src, const in
   for (int j = threadIdx.x; j < cols; j += blockDim.x) o[j] = s[j];
 }
 
+// dst[c][r] = src[r][c] for a [rows, cols] bf16 matrix, 32x32 tiles through
+// LDS (one-time layout change at load)
+__global__ void transpose_bf16_kernel(uint16_t *dst, const uint16_t *src, int rows, int cols) {
+  __shared__ uint16_t t[32][33];
+  const int c0 = blockIdx.x * 32, r0 = blockIdx.y * 32;
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;  // 256 threads: 8 rows a pass
+  for (int y = ty; y < 32; y += 8) {
+    const int r = r0 + y, c = c0 + tx;
+    if (r < rows && c < cols) t[y][tx] = src[(size_t)r * cols + c];
+  }
+  __syncthreads();
+  for (int y = ty; y < 32; y += 8) {
+    const int c = c0 + y, r = r0 + tx;
+    if (r < rows && c < cols) dst[(size_t)c * rows + r] = t[tx][y];
+  }
+}
+
 inline unsigned nblk(size_t n, unsigned b) { return (unsigned)((n + b - 1) / b); }
 
 }  // namespace
@@ -1156,6 +1173,14 @@ hipError_t launch_permute_rows(uint16_t *dst, const uint16_t *src, const int *pe
                                int cols, hipStream_t s) {
   if (rows <= 0) return hipSuccess;
   hipLaunchKernelGGL(permute_rows_kernel, dim3(rows), dim3(256), 0, s, dst, src, perm, cols);
+  return hipGetLastError();
+}
+
+hipError_t launch_transpose_bf16(uint16_t *dst, const uint16_t *src, int rows, int cols,
+                                 hipStream_t s) {
+  if (rows <= 0 || cols <= 0) return hipSuccess;
+  hipLaunchKernelGGL(transpose_bf16_kernel, dim3(nblk(cols, 32), nblk(rows, 32)), dim3(256), 0, s,
+                     dst, src, rows, cols);
   return hipGetLastError();
 }
 

@@ -25,6 +25,7 @@
 #include <math.h>
 #include <string.h>
 
+#include <algorithm>
 #include <chrono>
 #include <string>
 #include <vector>
@@ -93,6 +94,8 @@ struct myos_model {
   size_t pbuf_bytes = 0;
   PersistLayer *dlayers = nullptr;
   PersistArgs pargs{};            // all but tag_base / steps / pos0
+  bool persist_stream = false;    // the streamed kernel (myos_stream.hip) runs it
+  uint16_t *wdT = nullptr;        // streamed kernel: down transposed, [L][I][H]
   uint32_t tag_base = 1;          // tags below this value are spent
   uint32_t *err = nullptr;
   uint64_t *trace = nullptr;      // phase timestamps (myos_set_decode_trace)
@@ -409,28 +412,46 @@ int setup_persistent(myos_model *m) {
   a.max_seq = (int)m->max_seq;
   a.qkv_rows = (int)m->qkv_rows;
   a.eps = s.rms_eps;
-  if (m->kv_bf16 || !persist_device_ok(a)) return MYOS_OK;  // per-kernel path only
-  const size_t words[8] = {m->q_dim, 2 * m->kv_dim,
-                           persist_part_words(a.nq, a.max_seq, a.d), m->q_dim, s.hidden,
-                           s.intermediate, s.hidden, 2 * (size_t)persist_grid()};
+  if (m->kv_bf16) return MYOS_OK;  // per-kernel path only
+  // MYOS_PERSIST_KERNEL=stream selects the streamed kernel (myos_stream.hip)
+  const char *pk = getenv("MYOS_PERSIST_KERNEL");
+  const bool want_stream = pk && std::string(pk) == "stream";
+  a.tpd = nullptr;
+  m->persist_stream = want_stream && stream_device_ok(a);
+  if (!m->persist_stream && !persist_device_ok(a)) return MYOS_OK;
+  const size_t words[9] = {m->q_dim, 2 * m->kv_dim,
+                           std::max(persist_part_words(a.nq, a.max_seq, a.d),
+                                    stream_part_words(a.nq, a.max_seq, a.d)),
+                           m->q_dim, s.hidden,
+                           s.intermediate, s.hidden, 2 * (size_t)persist_grid(),
+                           m->persist_stream ? stream_tpd_words((int)s.hidden) : 0};
   size_t total = 0;
   for (size_t w : words) total += align256(w * 8);
   total += 256;  // error word
   HIP_TRY(hipMalloc((void **)&m->pbuf, total));
   HIP_TRY(hipMemsetAsync(m->pbuf, 0, total, m->stream));
   m->pbuf_bytes = total;
-  uint64_t **dst[8] = {&a.tq, &a.tkv, &a.tpart, &a.tatt, &a.txo, &a.th, &a.txd, &a.targ};
+  uint64_t **dst[9] = {&a.tq, &a.tkv, &a.tpart, &a.tatt, &a.txo, &a.th, &a.txd, &a.targ, &a.tpd};
   uint8_t *p = m->pbuf;
-  for (int i = 0; i < 8; i++) {
+  for (int i = 0; i < 9; i++) {
     *dst[i] = (uint64_t *)p;
     p += align256(words[i] * 8);
   }
   m->err = (uint32_t *)p;
   a.err = m->err;
   std::vector<PersistLayer> hl(s.num_layers);
+  const size_t dsz = s.intermediate * s.hidden;  // elements of one down matrix
+  if (m->persist_stream) {
+    // the streamed kernel reads down by columns: keep a transposed copy
+    HIP_TRY(hipMalloc((void **)&m->wdT, s.num_layers * dsz * 2));
+    for (size_t l = 0; l < s.num_layers; l++)
+      HIP_TRY(launch_transpose_bf16(m->wdT + l * dsz, m->layers[l].wd, (int)s.hidden,
+                                    (int)s.intermediate, m->stream));
+  }
   for (size_t l = 0; l < s.num_layers; l++) {
     const DevLayer &L = m->layers[l];
-    hl[l] = PersistLayer{L.ln1, L.wqkv, L.wo, L.ln2, L.wgu, L.wd, L.bqkv};
+    hl[l] = PersistLayer{L.ln1, L.wqkv, L.wo, L.ln2, L.wgu, L.wd, L.bqkv,
+                         m->wdT ? m->wdT + l * dsz : nullptr};
   }
   HIP_TRY(hipMalloc((void **)&m->dlayers, hl.size() * sizeof(PersistLayer)));
   HIP_TRY(hipMemcpy(m->dlayers, hl.data(), hl.size() * sizeof(PersistLayer),
@@ -479,7 +500,8 @@ int persist_decode(myos_model *m, size_t n) {
     a.trace = m->trace;
     a.trace_step = (uint32_t)m->trace_step;
   }
-  const hipError_t e = launch_decode_persistent(a, m->stream);
+  const hipError_t e = m->persist_stream ? launch_decode_stream(a, m->stream)
+                                         : launch_decode_persistent(a, m->stream);
   if (e == hipErrorCooperativeLaunchTooLarge || e == hipErrorInvalidConfiguration) {
     (void)hipGetLastError();
     return kLaunchRefused;  // nothing ran: the caller takes the per-kernel path
@@ -547,6 +569,7 @@ void myos_model_close(myos_model *m) {
   if (m->pf) (void)hipFree(m->pf);
   if (m->pbuf) (void)hipFree(m->pbuf);
   if (m->dlayers) (void)hipFree(m->dlayers);
+  if (m->wdT) (void)hipFree(m->wdT);
   if (m->trace) (void)hipFree(m->trace);
   if (m->host_state) (void)hipHostFree(m->host_state);
   if (m->stream) (void)hipStreamDestroy(m->stream);

@@ -52,6 +52,18 @@ def agree(got, ref, gaps):
     return len(ref)
 
 
+@pytest.fixture(params=["first", "stream"], autouse=True)
+def persist_kernel(request, monkeypatch):
+    """Every test runs with each cooperative decode kernel: the first
+    (myos_persistent.hip, the default) and the streamed one
+    (myos_stream.hip, MYOS_PERSIST_KERNEL=stream), chosen at model open."""
+    if request.param == "stream":
+        monkeypatch.setenv("MYOS_PERSIST_KERNEL", "stream")
+    else:
+        monkeypatch.delenv("MYOS_PERSIST_KERNEL", raising=False)
+    return request.param
+
+
 SMALL = [(256, 4, 2, 64, 512, 1000, 3), (128, 6, 1, 32, 384, 777, 2),
          (384, 12, 2, 32, 1000, 4099, 2), (512, 4, 1, 128, 1536, 2048, 2)]
 
