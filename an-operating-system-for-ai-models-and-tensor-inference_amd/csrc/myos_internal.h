@@ -111,7 +111,15 @@ struct GemmArgs {
   int kv_bf16, max_seq, q_dim, kv_dim, head_dim;
   // EPI_GU: writes h = silu(g)*u as hi/lo planes [M, N/2]
   uint16_t *h_hi, *h_lo;
+  // K-split partials [splits][M][N] f32 (gemm_ws_floats); null: one split
+  float *ws;
+  size_t ws_cap;               // floats at ws
+  int kps;                     // set by the launcher: K steps per split
 };
+// K splits launch_gemm uses for this shape (about one workgroup per CU), and
+// the partial-buffer floats they need (0 when one split)
+int gemm_splits(int M, int N, int K);
+size_t gemm_ws_floats(int M, int N, int K);
 hipError_t launch_gemm(const GemmArgs &a, GemvEpi epi, hipStream_t s);
 
 struct AttnPrefillArgs {

@@ -756,6 +756,84 @@ __device__ __forceinline__ u32x4 load_tile8(const uint16_t *src, int row, int ro
   return v;
 }
 
+// One output element of the GEMM epilogues; `partner` is column col ^ 1 of
+// the same row (the gate/up pair, the RoPE pair)
+template <int EPI>
+__device__ __forceinline__ void gemm_store(const GemmArgs &a, int row, int col, float c,
+                                           float partner) {
+  const int N = a.N;
+  if (EPI == EPI_STORE) {
+    a.y[(size_t)row * N + col] = c;
+  } else if (EPI == EPI_RESID) {
+    a.y[(size_t)row * N + col] += c;
+  } else if (EPI == EPI_GU) {
+    if ((col & 1) == 0) {
+      const size_t o = (size_t)row * (N >> 1) + (col >> 1);
+      split2(silu(c) * partner, a.h_hi + o, a.h_lo + o);
+    }
+  } else if (EPI == EPI_QKV) {
+    if ((col & 1) == 0) {
+      const int d = a.head_dim, half = d >> 1;
+      const int pos = a.start_pos + row;
+      const float y0 = c + a.bias[col], y1 = partner + a.bias[col + 1];
+      if (col < a.q_dim + a.kv_dim) {
+        const bool is_q = col < a.q_dim;
+        const int rr = is_q ? col : col - a.q_dim;
+        const int u = rr >> 1, head = u / half, p = u - head * half;
+        const float2 cs = a.rope[(size_t)pos * half + p];
+        const float o0 = y0 * cs.x - y1 * cs.y;
+        const float o1 = y1 * cs.x + y0 * cs.y;
+        if (is_q) {
+          float *qrow = a.q_out + (size_t)row * a.q_dim;
+          qrow[head * d + p] = o0;
+          qrow[head * d + p + half] = o1;
+        } else {
+          const size_t base = ((size_t)head * a.max_seq + pos) * d;
+          store_kv(a.kc, base + p, o0, a.kv_bf16);
+          store_kv(a.kc, base + p + half, o1, a.kv_bf16);
+        }
+      } else {
+        const int rr = col - a.q_dim - a.kv_dim;
+        const int head = rr / d, j = rr - head * d;
+        const size_t base = ((size_t)head * a.max_seq + pos) * d + j;
+        store_kv(a.vc, base, y0, a.kv_bf16);
+        store_kv(a.vc, base + 1, y1, a.kv_bf16);
+      }
+    }
+  }
+}
+
+// One K tile of both operands: A (hi, lo) 128 rows x 8 octets, W 64 x 8;
+// thread tid holds octets tid + it * kBlock
+struct GemmTile {
+  u32x4 ah[4], al[4], w[2];
+};
+__device__ __forceinline__ void gemm_load_tile(const GemmArgs &a, int m0, int n0, int k0, bool vec,
+                                               int tid, GemmTile &t) {
+#pragma unroll
+  for (int it = 0; it < 4; it++) {
+    const int v = tid + it * kBlock, r = v >> 3, o = v & 7;
+    t.ah[it] = load_tile8(a.a_hi, m0 + r, a.M, k0 + o * 8, a.K, vec);
+    t.al[it] = load_tile8(a.a_lo, m0 + r, a.M, k0 + o * 8, a.K, vec);
+  }
+#pragma unroll
+  for (int it = 0; it < 2; it++) {
+    const int v = tid + it * kBlock, r = v >> 3, o = v & 7;
+    t.w[it] = load_tile8(a.w, n0 + r, a.N, k0 + o * 8, a.K, vec);
+  }
+}
+
+// MFMA GEMM, C[M,N] = (A_hi + A_lo)[M,K] . W[N,K]^T, both operands K-contiguous.
+// Workgroup tile 128 (M) x 64 (N) x 64 (K); wave w owns rows 32w..32w+31 and
+// both 32-column halves: 2 accumulators of v_mfma_f32_32x32x16_bf16, each fed
+// by the hi and the lo term of A. Operand fragments: lane l holds row/col
+// (l % 32) and K-octet (l / 32) of a 16-wide K step, so A and W share the K
+// mapping; the 32x32 result sits at row 8*(i/4) + 4*(l/32) + i%4, col l%32.
+// The next K tile loads into registers while the current one is multiplied
+// (a deeper register pipeline measured slower: it halves occupancy).
+// blockIdx.z takes the K steps [z * kps, (z + 1) * kps): with more than one
+// split the tile goes to the partial buffer a.ws[z] and gemm_reduce_kernel
+// adds the splits in order and applies the epilogue.
 template <int EPI>
 __global__ void __launch_bounds__(kBlock) gemm_mfma_kernel(GemmArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t ahi_s[GBM * GLD];
@@ -764,6 +842,7 @@ __global__ void __launch_bounds__(kBlock) gemm_mfma_kernel(GemmArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int n0 = blockIdx.x * GBN, m0 = blockIdx.y * GBM;
   const int M = a.M, N = a.N, K = a.K;
+  const int kbeg = blockIdx.z * a.kps * GBK, kend = min(K, kbeg + a.kps * GBK);
   // 16-byte operand loads need K % 8 == 0 and 16-byte aligned bases
   const bool vec = (K & 7) == 0 && (((uintptr_t)a.a_hi | (uintptr_t)a.a_lo | (uintptr_t)a.w) & 15) == 0;
   f32x16 acc0, acc1;
@@ -772,20 +851,22 @@ __global__ void __launch_bounds__(kBlock) gemm_mfma_kernel(GemmArgs a) {
     acc0[i] = 0.f;
     acc1[i] = 0.f;
   }
-  for (int k0 = 0; k0 < K; k0 += GBK) {
-    // A tiles: 128 rows x 8 octets = 1024 vectors; W tile: 64 x 8 = 512
+  GemmTile t;
+  if (kbeg < kend) gemm_load_tile(a, m0, n0, kbeg, vec, tid, t);
+  for (int k0 = kbeg; k0 < kend; k0 += GBK) {
 #pragma unroll
     for (int it = 0; it < 4; it++) {
       const int v = tid + it * kBlock, r = v >> 3, o = v & 7;
-      *(u32x4 *)&ahi_s[r * GLD + o * 8] = load_tile8(a.a_hi, m0 + r, M, k0 + o * 8, K, vec);
-      *(u32x4 *)&alo_s[r * GLD + o * 8] = load_tile8(a.a_lo, m0 + r, M, k0 + o * 8, K, vec);
+      *(u32x4 *)&ahi_s[r * GLD + o * 8] = t.ah[it];
+      *(u32x4 *)&alo_s[r * GLD + o * 8] = t.al[it];
     }
 #pragma unroll
     for (int it = 0; it < 2; it++) {
       const int v = tid + it * kBlock, r = v >> 3, o = v & 7;
-      *(u32x4 *)&w_s[r * GLD + o * 8] = load_tile8(a.w, n0 + r, N, k0 + o * 8, K, vec);
+      *(u32x4 *)&w_s[r * GLD + o * 8] = t.w[it];
     }
     __syncthreads();
+    if (k0 + GBK < kend) gemm_load_tile(a, m0, n0, k0 + GBK, vec, tid, t);
 #pragma unroll
     for (int ks = 0; ks < GBK; ks += 16) {
       const int kk = ks + (lane >> 5) * 8;
@@ -802,7 +883,8 @@ __global__ void __launch_bounds__(kBlock) gemm_mfma_kernel(GemmArgs a) {
     }
     __syncthreads();
   }
-  const int d = a.head_dim, half = d >> 1;
+  const bool split = gridDim.z > 1;
+  float *ws = a.ws + (size_t)blockIdx.z * M * N;
 #pragma unroll
   for (int nh = 0; nh < 2; nh++) {
 #pragma unroll
@@ -812,46 +894,29 @@ __global__ void __launch_bounds__(kBlock) gemm_mfma_kernel(GemmArgs a) {
       const int col = n0 + nh * 32 + (lane & 31);
       const float partner = __shfl_xor(c, 1, kWave);  // column col ^ 1, same row
       if (row >= M || col >= N) continue;
-      if (EPI == EPI_STORE) {
-        a.y[(size_t)row * N + col] = c;
-      } else if (EPI == EPI_RESID) {
-        a.y[(size_t)row * N + col] += c;
-      } else if (EPI == EPI_GU) {
-        if ((col & 1) == 0) {
-          const size_t o = (size_t)row * (N >> 1) + (col >> 1);
-          split2(silu(c) * partner, a.h_hi + o, a.h_lo + o);
-        }
-      } else if (EPI == EPI_QKV) {
-        if ((col & 1) == 0) {
-          const int pos = a.start_pos + row;
-          const float y0 = c + a.bias[col], y1 = partner + a.bias[col + 1];
-          if (col < a.q_dim + a.kv_dim) {
-            const bool is_q = col < a.q_dim;
-            const int rr = is_q ? col : col - a.q_dim;
-            const int u = rr >> 1, head = u / half, p = u - head * half;
-            const float2 cs = a.rope[(size_t)pos * half + p];
-            const float o0 = y0 * cs.x - y1 * cs.y;
-            const float o1 = y1 * cs.x + y0 * cs.y;
-            if (is_q) {
-              float *qrow = a.q_out + (size_t)row * a.q_dim;
-              qrow[head * d + p] = o0;
-              qrow[head * d + p + half] = o1;
-            } else {
-              const size_t base = ((size_t)head * a.max_seq + pos) * d;
-              store_kv(a.kc, base + p, o0, a.kv_bf16);
-              store_kv(a.kc, base + p + half, o1, a.kv_bf16);
-            }
-          } else {
-            const int rr = col - a.q_dim - a.kv_dim;
-            const int head = rr / d, j = rr - head * d;
-            const size_t base = ((size_t)head * a.max_seq + pos) * d + j;
-            store_kv(a.vc, base, y0, a.kv_bf16);
-            store_kv(a.vc, base + 1, y1, a.kv_bf16);
-          }
-        }
-      }
+      if (split) ws[(size_t)row * N + col] = c;
+      else gemm_store<EPI>(a, row, col, c, partner);
     }
   }
+}
+
+// the K splits of gemm_mfma_kernel, added in split order, then the epilogue;
+// one thread per column pair (a last odd column stands alone)
+template <int EPI>
+__global__ void __launch_bounds__(kBlock) gemm_reduce_kernel(GemmArgs a, int splits) {
+  const int np = (a.N + 1) >> 1;
+  const size_t i = blockIdx.x * (size_t)kBlock + threadIdx.x;
+  if (i >= (size_t)a.M * np) return;
+  const int row = (int)(i / (size_t)np), col = 2 * (int)(i % (size_t)np);
+  const bool two = col + 1 < a.N;
+  const size_t MN = (size_t)a.M * a.N, off = (size_t)row * a.N + col;
+  float c0 = 0.f, c1 = 0.f;
+  for (int z = 0; z < splits; z++) {
+    c0 += a.ws[z * MN + off];
+    if (two) c1 += a.ws[z * MN + off + 1];
+  }
+  gemm_store<EPI>(a, row, col, c0, c1);
+  if (two) gemm_store<EPI>(a, row, col + 1, c1, c0);
 }
 
 // Causal prefill attention: workgroup = (query head, 32 queries); 8 lanes per
@@ -944,6 +1009,93 @@ __global__ void transpose_bf16_kernel(uint16_t *dst, const uint16_t *src, int ro
   for (int y = ty; y < 32; y += 8) {
     const int c = c0 + y, r = r0 + tx;
     if (r < rows && c < cols) dst[(size_t)c * rows + r] = t[tx][y];
+  }
+}
+
+// Causal prefill attention for head_dim D in {32, 64, 128}: workgroup = (query
+// head, 16 queries), 8 lanes per query each own D / 8 adjacent dims; keys and
+// values stream through LDS in tiles of 32. Per tile all 32 scores are formed
+// first, then the running max, the rescale of the partial output and the
+// probabilities (one online-softmax step per tile). Query i sits at position
+// start + i and sees keys <= it (GqaMask::Causal, gqa.rs:80-86).
+constexpr int kTq = 16, kTk = 32;
+template <int D>
+__global__ void __launch_bounds__(kTq * 8) attn_prefill_tiled_kernel(AttnPrefillArgs a) {
+  constexpr int DL = D / 8;
+  __shared__ __attribute__((aligned(16))) float k_s[kTk * D];
+  __shared__ __attribute__((aligned(16))) float v_s[kTk * D];
+  const int h = blockIdx.x, g = h / (a.nq / a.nkv);
+  const int tid = threadIdx.x, qi = blockIdx.y * kTq + (tid >> 3), j = tid & 7;
+  const bool active = qi < a.M;
+  const int qpos = a.start_pos + (active ? qi : a.M - 1);
+  const int last_pos = a.start_pos + min(a.M - 1, (int)(blockIdx.y + 1) * kTq - 1);
+  const float scale = 1.0f / sqrtf((float)D);
+  const int qd = a.nq * D;
+  float q[DL], o[DL];
+#pragma unroll
+  for (int e = 0; e < DL; e++) {
+    q[e] = active ? a.q[(size_t)qi * qd + h * D + j * DL + e] : 0.f;
+    o[e] = 0.f;
+  }
+  float mx = -INFINITY, l = 0.f;
+  for (int t0 = 0; t0 <= last_pos; t0 += kTk) {
+    const int nt = min(kTk, last_pos + 1 - t0);
+    __syncthreads();
+    // the tile's K and V rows, 4 floats per load
+    const size_t kv0 = ((size_t)g * a.max_seq + t0) * D;
+    for (int i = tid * 4; i < nt * D; i += kTq * 8 * 4) {
+      float4 kv, vv;
+      if (a.kv_bf16) {
+        const uint2 kb = *(const uint2 *)((const uint16_t *)a.kc + kv0 + i);
+        const uint2 vb = *(const uint2 *)((const uint16_t *)a.vc + kv0 + i);
+        kv = make_float4(bf_lo(kb.x), bf_hi(kb.x), bf_lo(kb.y), bf_hi(kb.y));
+        vv = make_float4(bf_lo(vb.x), bf_hi(vb.x), bf_lo(vb.y), bf_hi(vb.y));
+      } else {
+        kv = *(const float4 *)((const float *)a.kc + kv0 + i);
+        vv = *(const float4 *)((const float *)a.vc + kv0 + i);
+      }
+      *(float4 *)(k_s + i) = kv;
+      *(float4 *)(v_s + i) = vv;
+    }
+    __syncthreads();
+    float sc[kTk];
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < kTk; t++) {
+      float s = 0.f;
+      if (t < nt) {
+        const float *kr = k_s + t * D + j * DL;
+#pragma unroll
+        for (int e = 0; e < DL; e++) s = fmaf(q[e], kr[e], s);
+      }
+      s = group_sum<8>(s) * scale;
+      sc[t] = (t < nt && t0 + t <= qpos) ? s : -INFINITY;
+      tmax = fmaxf(tmax, sc[t]);
+    }
+    const float mnew = fmaxf(mx, tmax);
+    if (mnew == -INFINITY) continue;  // nothing visible yet
+    const float corr = expf(mx - mnew);
+    float psum = 0.f;
+#pragma unroll
+    for (int e = 0; e < DL; e++) o[e] *= corr;
+#pragma unroll
+    for (int t = 0; t < kTk; t++) {
+      const float p = expf(sc[t] - mnew);  // masked: exp(-inf) = 0
+      psum += p;
+      if (t < nt) {
+        const float *vr = v_s + t * D + j * DL;
+#pragma unroll
+        for (int e = 0; e < DL; e++) o[e] = fmaf(p, vr[e], o[e]);
+      }
+    }
+    l = l * corr + psum;
+    mx = mnew;
+  }
+  if (!active) return;
+#pragma unroll
+  for (int e = 0; e < DL; e++) {
+    const size_t idx = (size_t)qi * qd + h * D + j * DL + e;
+    split2(o[e] / l, a.out_hi + idx, a.out_lo + idx);
   }
 }
 
@@ -1139,22 +1291,45 @@ hipError_t launch_split_rows(const float *X, size_t n, uint16_t *hi, uint16_t *l
   return hipGetLastError();
 }
 
-hipError_t launch_gemm(const GemmArgs &a, GemvEpi epi, hipStream_t s) {
-  if (a.M <= 0 || a.N <= 0) return hipSuccess;
-  dim3 grid(nblk((size_t)a.N, GBN), nblk((size_t)a.M, GBM));
+int gemm_splits(int M, int N, int K) {
+  const int tiles = (int)(nblk((size_t)N, GBN) * nblk((size_t)M, GBM));
+  const int ksteps = (K + GBK - 1) / GBK;
+  // about two workgroups per CU, so one's operand loads overlap the other's
+  // MFMAs (measured at M = 128: one per CU 4 % slower, three 11 % slower)
+  int sp = (512 + tiles - 1) / tiles;
+  if (sp > ksteps) sp = ksteps;
+  if (sp < 1) sp = 1;
+  const int kps = (ksteps + sp - 1) / sp;
+  return (ksteps + kps - 1) / kps;
+}
+
+size_t gemm_ws_floats(int M, int N, int K) {
+  const int sp = gemm_splits(M, N, K);
+  return sp > 1 ? (size_t)sp * M * N : 0;
+}
+
+hipError_t launch_gemm(const GemmArgs &args, GemvEpi epi, hipStream_t s) {
+  if (args.M <= 0 || args.N <= 0) return hipSuccess;
+  GemmArgs a = args;
+  const int ksteps = (a.K + GBK - 1) / GBK;
+  int splits = gemm_splits(a.M, a.N, a.K);
+  if (!a.ws || a.ws_cap < (size_t)splits * a.M * a.N) splits = 1;  // no room for partials
+  a.kps = (ksteps + splits - 1) / splits;
+  if (a.kps < 1) a.kps = 1;
+  dim3 grid(nblk((size_t)a.N, GBN), nblk((size_t)a.M, GBM), splits);
+  const unsigned rgrid = nblk((size_t)a.M * ((a.N + 1) >> 1), kBlock);
   switch (epi) {
-    case EPI_STORE:
-      hipLaunchKernelGGL(gemm_mfma_kernel<EPI_STORE>, grid, dim3(kBlock), 0, s, a);
-      break;
-    case EPI_RESID:
-      hipLaunchKernelGGL(gemm_mfma_kernel<EPI_RESID>, grid, dim3(kBlock), 0, s, a);
-      break;
-    case EPI_GU:
-      hipLaunchKernelGGL(gemm_mfma_kernel<EPI_GU>, grid, dim3(kBlock), 0, s, a);
-      break;
-    case EPI_QKV:
-      hipLaunchKernelGGL(gemm_mfma_kernel<EPI_QKV>, grid, dim3(kBlock), 0, s, a);
-      break;
+#define MYOS_GEMM_CASE(E)                                                          \
+  case E:                                                                         \
+    hipLaunchKernelGGL(gemm_mfma_kernel<E>, grid, dim3(kBlock), 0, s, a);         \
+    if (splits > 1)                                                               \
+      hipLaunchKernelGGL(gemm_reduce_kernel<E>, dim3(rgrid), dim3(kBlock), 0, s, a, splits); \
+    break;
+    MYOS_GEMM_CASE(EPI_STORE)
+    MYOS_GEMM_CASE(EPI_RESID)
+    MYOS_GEMM_CASE(EPI_GU)
+    MYOS_GEMM_CASE(EPI_QKV)
+#undef MYOS_GEMM_CASE
     default:
       return hipErrorInvalidValue;
   }
@@ -1163,6 +1338,16 @@ hipError_t launch_gemm(const GemmArgs &a, GemvEpi epi, hipStream_t s) {
 
 hipError_t launch_attn_prefill(const AttnPrefillArgs &a, hipStream_t s) {
   if (a.head_dim > kMaxHeadDim) return hipErrorInvalidValue;
+  // 16-byte tile loads: the cache rows and q must be aligned to 4 elements
+  if (a.head_dim == 128 || a.head_dim == 64 || a.head_dim == 32) {
+    dim3 tg(a.nq, nblk((size_t)a.M, kTq));
+    switch (a.head_dim) {
+      case 128: hipLaunchKernelGGL(attn_prefill_tiled_kernel<128>, tg, dim3(kTq * 8), 0, s, a); break;
+      case 64: hipLaunchKernelGGL(attn_prefill_tiled_kernel<64>, tg, dim3(kTq * 8), 0, s, a); break;
+      default: hipLaunchKernelGGL(attn_prefill_tiled_kernel<32>, tg, dim3(kTq * 8), 0, s, a); break;
+    }
+    return hipGetLastError();
+  }
   dim3 grid(a.nq, nblk((size_t)a.M, kPqPerBlock));
   const size_t smem = sizeof(float) * 2 * kPkTile * a.head_dim;
   hipLaunchKernelGGL(attn_prefill_kernel, grid, dim3(kBlock), smem, s, a);

@@ -81,6 +81,8 @@ struct myos_model {
   float *pX = nullptr, *pQ = nullptr;
   uint16_t *pAhi = nullptr, *pAlo = nullptr, *pHhi = nullptr, *pHlo = nullptr;
   uint32_t *ptok = nullptr;
+  float *pws = nullptr;           // GEMM K-split partials
+  size_t pws_cap = 0;
   // graph + timing
   bool use_graph = true;
   hipGraphExec_t graph = nullptr;   // one decode step
@@ -360,7 +362,14 @@ int ensure_prefill(myos_model *m, size_t rows) {
   const size_t bx = align256(rows * H * 4), bq = align256(rows * Q * 4);
   const size_t ba = align256(rows * (H > Q ? H : Q) * 2), bh = align256(rows * I * 2);
   const size_t bt = align256(rows * 4);
-  const size_t total = bx + bq + 2 * ba + 2 * bh + bt;
+  // K-split partials of the four projections
+  const int R = (int)rows;
+  size_t wsf = gemm_ws_floats(R, (int)m->qkv_rows, (int)H);
+  wsf = std::max(wsf, gemm_ws_floats(R, (int)H, (int)Q));
+  wsf = std::max(wsf, gemm_ws_floats(R, (int)m->gu_rows, (int)H));
+  wsf = std::max(wsf, gemm_ws_floats(R, (int)H, (int)I));
+  const size_t bw = align256(wsf * 4);
+  const size_t total = bx + bq + 2 * ba + 2 * bh + bt + bw;
   HIP_TRY(hipMalloc((void **)&m->pf, total));
   uint8_t *p = m->pf;
   m->pX = (float *)p;
@@ -376,6 +385,9 @@ int ensure_prefill(myos_model *m, size_t rows) {
   m->pHlo = (uint16_t *)p;
   p += bh;
   m->ptok = (uint32_t *)p;
+  p += bt;
+  m->pws = wsf ? (float *)p : nullptr;
+  m->pws_cap = wsf;
   m->pf_rows = rows;
   return MYOS_OK;
 }
@@ -848,6 +860,8 @@ int myos_prefill(myos_model *m, const uint32_t *tokens, size_t n) {
     g.q_dim = (int)m->q_dim;
     g.kv_dim = (int)m->kv_dim;
     g.head_dim = (int)s.head_dim;
+    g.ws = m->pws;
+    g.ws_cap = m->pws_cap;
     HIP_TRY(launch_gemm(g, EPI_QKV, st));
 
     AttnPrefillArgs ap;
@@ -873,6 +887,8 @@ int myos_prefill(myos_model *m, const uint32_t *tokens, size_t n) {
     o.N = H;
     o.K = (int)m->q_dim;
     o.y = m->pX;
+    o.ws = m->pws;
+    o.ws_cap = m->pws_cap;
     HIP_TRY(launch_gemm(o, EPI_RESID, st));
 
     HIP_TRY(launch_rmsnorm_rows_split(m->pX, L.ln2, s.rms_eps, M, H, m->pAhi, m->pAlo, st));
@@ -885,6 +901,8 @@ int myos_prefill(myos_model *m, const uint32_t *tokens, size_t n) {
     gu.K = H;
     gu.h_hi = m->pHhi;
     gu.h_lo = m->pHlo;
+    gu.ws = m->pws;
+    gu.ws_cap = m->pws_cap;
     HIP_TRY(launch_gemm(gu, EPI_GU, st));
 
     GemmArgs dn{};
@@ -895,6 +913,8 @@ int myos_prefill(myos_model *m, const uint32_t *tokens, size_t n) {
     dn.N = H;
     dn.K = I;
     dn.y = m->pX;
+    dn.ws = m->pws;
+    dn.ws_cap = m->pws_cap;
     HIP_TRY(launch_gemm(dn, EPI_RESID, st));
   }
   const float *last = m->pX + (size_t)(M - 1) * H;

@@ -90,6 +90,14 @@ int myos_gemm_bf16(float *y, size_t y_len, const uint16_t *w, size_t w_len, cons
     (void)hipFreeAsync(hi, s);
     return MYOS_E_HIP;
   }
+  // partials of the K splits (none when the grid already fills the device)
+  const size_t wsf = gemm_ws_floats((int)batch, (int)m, (int)k);
+  float *ws = nullptr;
+  if (wsf && hipMallocAsync((void **)&ws, wsf * 4, s) != hipSuccess) {
+    (void)hipFreeAsync(hi, s);
+    (void)hipFreeAsync(lo, s);
+    return MYOS_E_HIP;
+  }
   hipError_t e = launch_split_rows(x, x_need, hi, lo, s);
   if (e == hipSuccess) {
     GemmArgs g{};
@@ -100,10 +108,13 @@ int myos_gemm_bf16(float *y, size_t y_len, const uint16_t *w, size_t w_len, cons
     g.N = (int)m;
     g.K = (int)k;
     g.y = y;
+    g.ws = ws;
+    g.ws_cap = wsf;
     e = launch_gemm(g, EPI_STORE, s);
   }
   hipError_t f1 = hipFreeAsync(hi, s), f2 = hipFreeAsync(lo, s);
-  if (e == hipSuccess) e = f1 != hipSuccess ? f1 : f2;
+  hipError_t f3 = ws ? hipFreeAsync(ws, s) : hipSuccess;
+  if (e == hipSuccess) e = f1 != hipSuccess ? f1 : f2 != hipSuccess ? f2 : f3;
   return hip_status(e);
 }
 
