@@ -192,32 +192,67 @@ __device__ bool tgather_lin(const uint64_t *src, int n, uint32_t tag, float *dst
 }
 
 // ---- row tiles -----------------------------------------------------------------
+// Weight rows load through a buffer descriptor of the matrix with the row's
+// byte offset in a scalar register and one shared lane offset, so no per-row
+// 64-bit lane address stays live while a row is in flight.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t wrsrc(const uint16_t *W) {
+  return __builtin_amdgcn_make_buffer_rsrc((void *)W, (short)0, 0x7fffffff, 0x00020000);
+}
+
+// row `row` of a [rows, k] bf16 matrix, 8 columns per chunk, chunk lane + 64 i
+// in t[i]; `valid` and `row` are wave-uniform
 template <int C>
 __device__ __forceinline__ void ldrow(u32x4 (&t)[C], const uint16_t *W, int k, int row, bool valid,
                                       int lane) {
   const int nch = k >> 3;
-  const u32x4 *rp = (const u32x4 *)(W + (size_t)(valid ? row : 0) * k);
+  const __amdgpu_buffer_rsrc_t rs = wrsrc(W);
+  const int soff = valid ? row * k * 2 : 0;
 #pragma unroll
   for (int i = 0; i < C; i++) {
     const int c = lane + i * 64;
     const u32x4 zero = {0u, 0u, 0u, 0u};
-    t[i] = (valid && c < nch) ? __builtin_nontemporal_load(rp + c) : zero;
+    t[i] = (valid && c < nch) ? __builtin_amdgcn_raw_buffer_load_b128(rs, lane * 16 + i * 1024, soff, 2)
+                              : zero;
   }
 }
 
-// Stream one row into LDS with direct (DMA) loads: chunk c of the row lands at
-// dst + 16 c. `dst` must be wave-uniform; no registers hold the row meanwhile.
-// The compiler waits for these loads before the wave's next LDS read.
-__device__ __forceinline__ void dma_row(const uint16_t *W, int k, int row, bool valid, uint8_t *dst,
-                                        int lane) {
+// ldrow with every load issued: the row is clamped to `last` and each lane's
+// chunk to the row's last one (dotrow ignores chunks past the row), so the
+// number of loads in flight is the same on every path and a wait for an
+// older tile can leave the younger ones in flight.
+template <int C>
+__device__ __forceinline__ void ldrow_all(u32x4 (&t)[C], const uint16_t *W, int k, int row, int last,
+                                          int lane) {
   const int nch = k >> 3;
-  const u32x4 *rp = (const u32x4 *)(W + (size_t)(valid ? row : 0) * k);
-  for (int i = 0; i * 64 < nch; i++) {
+  const __amdgpu_buffer_rsrc_t rs = wrsrc(W);
+  const int soff = min(row, last) * k * 2;
+#pragma unroll
+  for (int i = 0; i < C; i++) {
+    const int c = min(lane + i * 64, nch - 1);
+    t[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, c * 16, soff, 2);
+  }
+}
+
+// Part `part` of `nparts` of one row streamed into LDS with direct (DMA)
+// loads: chunk c of the row lands at dst + 16 c, and this part covers the
+// 1 KB wave loads [part * per, (part + 1) * per), so a row's bytes can be
+// spread over several waits. `dst` must be wave-uniform; no registers hold
+// the row meanwhile. The compiler waits for these loads before the wave's
+// next LDS access.
+__device__ __forceinline__ void dma_row_part(const uint16_t *W, int k, int row, uint8_t *dst,
+                                             int lane, int part, int nparts) {
+  const int nch = k >> 3;
+  const int nld = (nch + 63) >> 6, per = (nld + nparts - 1) / nparts;
+  const int i0 = part * per, i1 = min(i0 + per, nld);
+  const __amdgpu_buffer_rsrc_t rs = wrsrc(W);
+  // the 1 KB step rides in the scalar offset: one lane offset serves every load
+  const int soff = row * k * 2;
+  for (int i = i0; i < i1; i++) {
     const int c = lane + i * 64;
-    if (valid && c < nch)
-      __builtin_amdgcn_global_load_lds((const void *)(rp + c),
-                                       (__attribute__((address_space(3))) void *)(dst + i * 1024),
-                                       16, 0, 2 /* nt */);
+    if (c < nch)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rs, (__attribute__((address_space(3))) void *)(dst + i * 1024), 16, lane * 16,
+          soff + i * 1024, 0, 2 /* nt */);
   }
 }
 
@@ -225,6 +260,7 @@ __device__ __forceinline__ void dma_row(const uint16_t *W, int k, int row, bool 
 __device__ __forceinline__ float dotrow_lds(const uint8_t *wl, const float *x, int k, int lane) {
   const int nch = k >> 3;
   float s = 0.f;
+#pragma unroll 4
   for (int c = lane; c < nch; c += 64) {
     const u32x4 w = *(const u32x4 *)(wl + c * 16);
     const float4 x0 = *(const float4 *)(x + c * 8), x1 = *(const float4 *)(x + c * 8 + 4);
@@ -265,23 +301,158 @@ __device__ __forceinline__ float dotrow(const u32x4 (&t)[C], const float *x, int
   return wave_sum(s);
 }
 
-// x <- g * (x * 1/sqrt(mean(x^2) + eps)) in LDS (rmsnorm_bf16_weight,
-// crates/tensor_core/src/bf16.rs:231-270, with a tree sum)
-__device__ void rmsnorm_lds(float *x, const uint16_t *g, int n, float eps, float *red) {
-  float ss = 0.f;
-  for (int j = threadIdx.x; j < n; j += NT) ss += x[j] * x[j];
-  ss = wave_sum(ss);
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
-  __syncthreads();
-  float tot = 0.f;
+// Sum over aligned groups of S lanes, S = 8, 16 or 32 (wave-uniform). For
+// S <= 16 every lane of a group holds its total; for S = 32 lanes 16-31 and
+// 48-63 do.
+__device__ __forceinline__ float seg_sum(float v, int S) {
+  v += dpp<0xB1>(v, 0.f);
+  v += dpp<0x4E>(v, 0.f);
+  v += dpp<0x141>(v, 0.f);
+  if (S >= 16) v += dpp<0x140>(v, 0.f);
+  if (S >= 32) v += dpp<0x142, 0xA>(v, 0.f);
+  return v;
+}
+__device__ __forceinline__ bool seg_leader(int lane, int S) {
+  return (lane & (S - 1)) == (S == 32 ? 16 : 0);
+}
+
+// this lane's chunks of x (chunk lane + 64 i, 8 floats each) in registers,
+// read from LDS once for every row a phase multiplies
+template <int C>
+__device__ __forceinline__ void load_x(float4 (&xr)[C][2], const float *x, int k, int lane) {
+  const int nch = k >> 3;
 #pragma unroll
-  for (int w = 0; w < NW; w++) tot += red[w];
-  const float inv = 1.0f / sqrtf(tot / (float)n + eps);
-  for (int j = threadIdx.x; j < n; j += NT) x[j] = bf16f(g[j]) * (x[j] * inv);
-  __syncthreads();
+  for (int i = 0; i < C; i++) {
+    const int c = lane + i * 64;
+    const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+    xr[i][0] = c < nch ? *(const float4 *)(x + c * 8) : z;
+    xr[i][1] = c < nch ? *(const float4 *)(x + c * 8 + 4) : z;
+  }
+}
+
+// dotrow with x from load_x
+template <int C>
+__device__ __forceinline__ float dotrow_x(const u32x4 (&t)[C], const float4 (&xr)[C][2], int k,
+                                          int lane) {
+  const int nch = k >> 3;
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < C; i++) {
+    const int c = lane + i * 64;
+    if (c < nch) {
+      const float4 x0 = xr[i][0], x1 = xr[i][1];
+      const u32x4 w = t[i];
+      s = fmaf(bf_lo(w.x), x0.x, s);
+      s = fmaf(bf_hi(w.x), x0.y, s);
+      s = fmaf(bf_lo(w.y), x0.z, s);
+      s = fmaf(bf_hi(w.y), x0.w, s);
+      s = fmaf(bf_lo(w.z), x1.x, s);
+      s = fmaf(bf_hi(w.z), x1.y, s);
+      s = fmaf(bf_lo(w.w), x1.z, s);
+      s = fmaf(bf_hi(w.w), x1.w, s);
+    }
+  }
+  return wave_sum(s);
+}
+
+// ---- normalised x in registers, split for bf16 dot products -------------------
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ float dot2(uint32_t w, uint32_t x, float acc) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w), __builtin_bit_cast(bf16x2, x),
+                                         acc, false);
+}
+// f32 -> bf16 bits, round to nearest even (finite inputs)
+__device__ __forceinline__ uint32_t bf16_rne(float f) {
+  const uint32_t u = __float_as_uint(f);
+  return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+}
+// This lane's chunks of x (chunk lane + 64 i, 8 columns each) as bf16 pairs
+// x = hi + lo: hi is x rounded to bf16, lo the remainder rounded to bf16, so
+// hi + lo carries 16 significant bits of x. A weight pair times (hi + lo) is
+// two v_dot2 steps accumulated in f32: half the VALU work of unpacking the
+// weights and multiplying in f32.
+template <int C>
+struct XPairs {
+  uint32_t h[C][4], l[C][4];
+};
+
+// Wave-local RMSNorm of x (rmsnorm_bf16_weight, crates/tensor_core/src/bf16.rs:
+// 231-270, with a tree sum): the wave's lanes hold every column of x (lane +
+// 64 i covers all chunks when k <= 512 C), so one wave_sum gives the mean
+// square without a barrier. `gw` holds the gains of this lane's chunks.
+// Returns the normalised chunks in f32 (xr) and split into pairs (xp).
+template <int C>
+__device__ __forceinline__ void norm_x(float4 (&xr)[C][2], XPairs<C> &xp, const float *x,
+                                       const u32x4 (&gw)[C], int k, float eps, int lane) {
+  load_x<C>(xr, x, k, lane);
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < C; i++) {
+    const float4 a = xr[i][0], b = xr[i][1];
+    ss += a.x * a.x + a.y * a.y + a.z * a.z + a.w * a.w + b.x * b.x + b.y * b.y + b.z * b.z +
+          b.w * b.w;
+  }
+  const float inv = 1.0f / sqrtf(wave_sum(ss) / (float)k + eps);
+#pragma unroll
+  for (int i = 0; i < C; i++) {
+    float v[8] = {xr[i][0].x, xr[i][0].y, xr[i][0].z, xr[i][0].w,
+                  xr[i][1].x, xr[i][1].y, xr[i][1].z, xr[i][1].w};
+    const uint32_t g[4] = {gw[i].x, gw[i].y, gw[i].z, gw[i].w};
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const float a = bf_lo(g[j]) * (v[2 * j] * inv), b = bf_hi(g[j]) * (v[2 * j + 1] * inv);
+      v[2 * j] = a;
+      v[2 * j + 1] = b;
+      const uint32_t ha = bf16_rne(a), hb = bf16_rne(b);
+      const uint32_t la = bf16_rne(a - __uint_as_float(ha << 16));
+      const uint32_t lb = bf16_rne(b - __uint_as_float(hb << 16));
+      xp.h[i][j] = ha | (hb << 16);
+      xp.l[i][j] = la | (lb << 16);
+    }
+    xr[i][0] = make_float4(v[0], v[1], v[2], v[3]);
+    xr[i][1] = make_float4(v[4], v[5], v[6], v[7]);
+  }
+}
+
+// gains of this lane's chunks (8 bf16 per chunk), loaded ahead of the wait
+template <int C>
+__device__ __forceinline__ void load_gw(u32x4 (&gw)[C], const uint16_t *g, int k, int lane) {
+  const int nch = k >> 3;
+#pragma unroll
+  for (int i = 0; i < C; i++) {
+    const int c = lane + i * 64;
+    const u32x4 zero = {0u, 0u, 0u, 0u};
+    gw[i] = c < nch ? *(const u32x4 *)(g + c * 8) : zero;
+  }
+}
+
+// one row (held 8 columns per chunk per lane) times the split x
+template <int C>
+__device__ __forceinline__ float dotrow_p(const u32x4 (&t)[C], const XPairs<C> &xp) {
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < C; i++) {
+    const u32x4 w = t[i];
+    s = dot2(w.x, xp.h[i][0], s);
+    s = dot2(w.x, xp.l[i][0], s);
+    s = dot2(w.y, xp.h[i][1], s);
+    s = dot2(w.y, xp.l[i][1], s);
+    s = dot2(w.z, xp.h[i][2], s);
+    s = dot2(w.z, xp.l[i][2], s);
+    s = dot2(w.w, xp.h[i][3], s);
+    s = dot2(w.w, xp.l[i][3], s);
+  }
+  return wave_sum(s);
 }
 
 __device__ __forceinline__ float silu(float z) { return z / (1.0f + expf(-z)); }
+
+// The value itself, through an empty volatile asm: the compiler cannot treat
+// it (or anything computed from it) as loop-invariant.
+__device__ __forceinline__ int opaque(int v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
 
 // phase timestamps of one step (100 MHz device clock), thread 0 of each
 // workgroup: slot 0 token chosen; 1 + 5 l + {0 x ready, 1 attention items
@@ -298,13 +469,16 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
   float *att = xs + MAXH;       // [MAXH] attention output
   float *big = att + MAXH;      // phase scratch: h [I] / attention staging / merge weights
   uint8_t *wdl = (uint8_t *)(xs + a.lds_wd);  // [rows per workgroup][I] bf16 down rows
-  __shared__ float red[NW * 2];
   __shared__ float xl[NW];      // this workgroup's rows of the residual stream
   __shared__ int fail_s;
   __shared__ uint32_t tok_s;
   __shared__ float2 best_s[NW];
 
-  const int tid = threadIdx.x, lane = tid & 63, wg = blockIdx.x;
+  // tid and lane are re-derived at the top of every step and layer (see
+  // opaque), so per-lane values computed from them are not hoisted out of
+  // the loops and held in registers for the whole launch
+  int tid = threadIdx.x, lane = tid & 63;
+  const int wg = blockIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int H = a.H, I = a.I, d = a.d, half = d >> 1, gq = a.nq / a.nkv;
   const int qdim = a.nq * d, kvdim = a.nkv * d;
@@ -327,21 +501,55 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
   if (tid < NW) xl[tid] = 0.f;
   __syncthreads();
 
-  // weight tiles held in registers across phases
+  // Weight rows held on chip across phases: this wave's QKV pair, o row and
+  // gate/up pairs in registers, its down row in LDS. Loads run up to a layer
+  // ahead of their use, spread over the four waits of a layer (h, x,
+  // attention, X_o) so that HBM streams through the whole dependency chain:
+  //   after gate/up(l):  QKV(l+1), gate/up slots 0, 1 of l+1
+  //   after down(l):     down parts 0, 1 of l+1
+  //   after merge(l):    o(l), gate/up slot 2 of l
+  //   after o(l):        gate/up slots 3, 4 of l, down part 2 of l
+  // Layer 0's first share loads after the head instead, so that no weight
+  // row is live across the head's own tiles; the attention items (the other
+  // register peak) see only slots 0 and 1 live.
+  // Each wait re-polls with vector loads, so it also waits for every load
+  // issued before it, and a wave that issues more loads than the CU's memory
+  // queue holds stalls at the issue itself: each wait gets about a quarter
+  // of the layer's bytes, issued after the phase's arithmetic.
   u32x4 wq0[HC], wq1[HC], wo[HC];
-  u32x4 gA0[HC], gA1[HC], gB0[HC], gB1[HC];  // gate/up pairs, two stages in flight
+  u32x4 gu[GPMAX][2][HC];  // gate/up slot p: rows (2i, 2i+1) = (gate_i, up_i)
+  uint8_t *wd_s = wdl + (size_t)wave * I * 2;  // this wave's down row
 
-  auto issue_qo = [&](int l) {
-    const PersistLayer &L = a.layers[l];
-    ldrow<HC>(wq0, L.wqkv, H, qrow, has_q, lane);
-    ldrow<HC>(wq1, L.wqkv, H, qrow + 1, has_q, lane);
-    ldrow<HC>(wo, L.wo, qdim, xrow, has_x, lane);
-  };
-  // gate/up pair p of this wavefront (rows 2i, 2i+1 = gate_i, up_i)
+  // gate/up pair in slot p of this wavefront
   auto gu_row = [&](int p) { return g0 + 2 * (wave + p * NW); };
+  auto issue_q = [&](int l, bool v) {
+    const PersistLayer &L = a.layers[l];
+    ldrow<HC>(wq0, L.wqkv, H, qrow, v && has_q, lane);
+    ldrow<HC>(wq1, L.wqkv, H, qrow + 1, v && has_q, lane);
+  };
+  auto issue_o = [&](int l, bool v) { ldrow<HC>(wo, a.layers[l].wo, qdim, xrow, v && has_x, lane); };
+  auto issue_gu = [&](int l, bool v, int p) {
+    const int row = gu_row(p);
+    const bool ok = v && row < g1;
+    ldrow<HC>(gu[p][0], a.layers[l].wgu, H, row, ok, lane);
+    ldrow<HC>(gu[p][1], a.layers[l].wgu, H, row + 1, ok, lane);
+  };
+  auto issue_down = [&](int l, bool v, int part) {
+    if (v && has_x) dma_row_part(a.layers[l].wd, I, xrow, wd_s, lane, part, 3);
+  };
+  // what layer l needs loaded before its first wait
+  auto issue_first = [&](int l) {
+    issue_q(l, true);
+    issue_gu(l, true, 0);
+    issue_gu(l, true, 1);
+    issue_down(l, true, 0);
+    issue_down(l, true, 1);
+  };
 
-  issue_qo(0);
+  issue_first(0);
   for (uint32_t s = 0; s < a.steps; s++) {
+    tid = opaque(tid);
+    lane = tid & 63;
     const uint32_t pos = a.pos0 + s;
     const int seq = (int)pos + 1;
     const uint32_t tstep = a.tag_base + s * TPS;
@@ -395,23 +603,39 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
     }
 
     for (int l = 0; l < a.L; l++) {
+      tid = opaque(tid);
+      lane = tid & 63;
       const PersistLayer &L = a.layers[l];
       const uint32_t T = tstep + (uint32_t)l * kTPL;
       float *kc = a.kc + (size_t)l * a.layer_kv, *vc = a.vc + (size_t)l * a.layer_kv;
 
       // ---- QKV + bias + RoPE + KV store (tag T + P_QKV) ---------------------
+      // gains, bias and this pair's (cos, sin) load while x is awaited
+      u32x4 gw[HC];
+      load_gw<HC>(gw, L.ln1, H, lane);
+      const bool roped = qrow < qdim + kvdim;
+      const int qu = (roped && qrow >= qdim ? qrow - qdim : qrow) >> 1;
+      const int qhead = qu / half, qp = qu - qhead * half;
+      float qb0 = 0.f, qb1 = 0.f;
+      float2 qcs = make_float2(1.f, 0.f);
+      if (has_q) {
+        qb0 = L.bqkv[qrow];
+        qb1 = L.bqkv[qrow + 1];
+        if (roped) qcs = a.rope[(size_t)pos * half + qp];
+      }
       if (l > 0) tgather_lin<3>(a.txd, H, T - kTPL + P_XD, xs, a, &fail_s);
       mark(a, s, 1 + 5 * l);
-      rmsnorm_lds(xs, L.ln1, H, a.eps, red);
       if (has_q) {
-        const float y0 = dotrow<HC>(wq0, xs, H, lane), y1 = dotrow<HC>(wq1, xs, H, lane);
+        float4 xr[HC][2];
+        XPairs<HC> xp;
+        norm_x<HC>(xr, xp, xs, gw, H, a.eps, lane);
+        const float y0 = dotrow_x<HC>(wq0, xr, H, lane), y1 = dotrow_x<HC>(wq1, xr, H, lane);
         if (lane == 0) {
-          const float b0 = y0 + L.bqkv[qrow], b1 = y1 + L.bqkv[qrow + 1];
-          if (qrow < qdim + kvdim) {
+          const float b0 = y0 + qb0, b1 = y1 + qb1;
+          if (roped) {
             const bool is_q = qrow < qdim;
-            const int rr = is_q ? qrow : qrow - qdim;
-            const int u = rr >> 1, head = u / half, p = u - head * half;
-            const float2 cs = a.rope[(size_t)pos * half + p];
+            const int head = qhead, p = qp;
+            const float2 cs = qcs;
             const float o0 = b0 * cs.x - b1 * cs.y, o1 = b1 * cs.x + b0 * cs.y;
             if (is_q) {
               tput(a.tq + head * d + p, o0, T + P_QKV);
@@ -431,13 +655,19 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
             tput(a.tkv + kvdim + head * d + j, b0, T + P_QKV);
             tput(a.tkv + kvdim + head * d + j + 1, b1, T + P_QKV);
           }
-          // the cache rows must be complete before anything this workgroup
-          // publishes later: later steps read them without tags
-          __builtin_amdgcn_s_waitcnt(0);
+          // Later steps read the cache rows without tags, so they must be
+          // complete before anything this wave publishes later. Every later
+          // publish follows one of the wave's gathers, and the wait for a
+          // gather's loads (vmcnt 0) also waits for these stores.
         }
       }
 
       // ---- attention partials for (kv head, chunk) items (tag T + P_PART) ----
+      // Thread i = tid + u NT holds columns [4 j4, 4 j4 + 4) of position
+      // t = i / dq of the chunk (dq = d / 4 lanes per position), K in
+      // registers and V staged in LDS. A score is a dq-lane segmented sum;
+      // then wave h takes q head h: softmax over the chunk in its lanes and
+      // the V sum with each weight read back from the lane that holds it.
       const int nch = (seq + AC - 1) / AC;
       for (int it = wg; it < a.nkv * nch; it += NB) {
         const int g = it % a.nkv, c = it / a.nkv;
@@ -445,23 +675,24 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
         const bool has_cur = (int)pos < t0 + n;  // this step's row ends the chunk
         const int nold = has_cur ? n - 1 : n;
         float *q_s = big;                    // [gq][d]
-        float *k_s = q_s + gq * d;           // [AC][d + 1]
-        float *v_s = k_s + AC * (d + 1);     // [AC][d]
-        float *p_s = v_s + AC * d;           // [gq][AC]
-        float *ml = p_s + gq * AC;           // [gq][2]
+        float *kcur = q_s + gq * d;          // [d] this step's k row of head g
+        float *v_s = kcur + d;               // [AC][d]
+        float *p_s = v_s + AC * d;           // [gq][AC] scaled scores
+        const int dq = d >> 2, j4 = tid & (dq - 1);
         // cached rows (positions < pos, complete before this step) and the
         // tagged q heads + this step's k, v of head g, all in one round trip
         const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
             kc, (short)0, (int)(a.layer_kv * sizeof(float)), 0x00020000);
         const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
             vc, (short)0, (int)(a.layer_kv * sizeof(float)), 0x00020000);
-        const int dq = d >> 2;
         u32x4 kr[KV4], vr[KV4];
 #pragma unroll
         for (int u = 0; u < KV4; u++) {
-          const int i = tid + u * NT;
-          if (i < nold * dq) {
-            const int t = i / dq, j4 = i - t * dq;
+          const int t = (tid + u * NT) / dq;
+          const u32x4 zero = {0u, 0u, 0u, 0u};
+          kr[u] = zero;
+          vr[u] = zero;
+          if (t < nold) {
             const uint32_t off = (uint32_t)((((size_t)g * a.max_seq + t0 + t) * d + j4 * 4) * 4);
             kr[u] = __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 16);
             vr[u] = __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, 16);
@@ -492,18 +723,11 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
         }
 #pragma unroll
         for (int u = 0; u < KV4; u++) {
-          const int i = tid + u * NT;
-          if (i < nold * dq) {
-            const int t = i / dq, j4 = i - t * dq;
-            float *kd = k_s + t * (d + 1) + j4 * 4;
-            kd[0] = __uint_as_float(kr[u].x);
-            kd[1] = __uint_as_float(kr[u].y);
-            kd[2] = __uint_as_float(kr[u].z);
-            kd[3] = __uint_as_float(kr[u].w);
+          const int t = (tid + u * NT) / dq;
+          if (t < nold)
             *(float4 *)(v_s + t * d + j4 * 4) =
                 make_float4(__uint_as_float(vr[u].x), __uint_as_float(vr[u].y),
                             __uint_as_float(vr[u].z), __uint_as_float(vr[u].w));
-          }
         }
 #pragma unroll
         for (int u = 0; u < QW; u++) {
@@ -511,53 +735,66 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
           const float v = __uint_as_float((uint32_t)w[u]);
           if (i < nqw) q_s[i] = v;
           else if (i < nw) {
-            if (r < d) k_s[nold * (d + 1) + r] = v;
+            if (r < d) kcur[r] = v;
             else v_s[nold * d + r - d] = v;
           }
         }
         __syncthreads();
         const float scale = 1.0f / sqrtf((float)d);
-        for (int i = tid; i < gq * n; i += NT) {
-          const int h = i / n, t = i - h * n;
-          const float *qh = q_s + h * d, *kt = k_s + t * (d + 1);
-          float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
-          for (int j = 0; j < d; j += 4) {
-            s0 = fmaf(qh[j], kt[j], s0);
-            s1 = fmaf(qh[j + 1], kt[j + 1], s1);
-            s2 = fmaf(qh[j + 2], kt[j + 2], s2);
-            s3 = fmaf(qh[j + 3], kt[j + 3], s3);
+#pragma unroll
+        for (int u = 0; u < KV4; u++) {
+          const int t = (tid + u * NT) / dq;
+          float4 k4 = make_float4(__uint_as_float(kr[u].x), __uint_as_float(kr[u].y),
+                                  __uint_as_float(kr[u].z), __uint_as_float(kr[u].w));
+          if (t >= nold) k4 = t < n ? *(const float4 *)(kcur + j4 * 4) : make_float4(0.f, 0.f, 0.f, 0.f);
+          float4 q4s[8];
+#pragma unroll
+          for (int h = 0; h < 8; h++)
+            if (h < gq) q4s[h] = *(const float4 *)(q_s + h * d + j4 * 4);
+#pragma unroll
+          for (int h = 0; h < 8; h++) {
+            if (h >= gq) break;
+            const float4 q4 = q4s[h];
+            float sc = q4.x * k4.x;
+            sc = fmaf(q4.y, k4.y, sc);
+            sc = fmaf(q4.z, k4.z, sc);
+            sc = fmaf(q4.w, k4.w, sc);
+            sc = seg_sum(sc, dq);
+            if (t < n && seg_leader(lane, dq)) p_s[h * AC + t] = sc * scale;
           }
-          p_s[h * AC + t] = ((s0 + s1) + (s2 + s3)) * scale;
         }
         __syncthreads();
-        for (int h = wave; h < gq; h += NW) {
+        if (wave < gq) {
+          const int h = wave;
           const float sc = lane < n ? p_s[h * AC + lane] : -INFINITY;
           const float mx = wave_max(sc);
           const float e = lane < n ? expf(sc - mx) : 0.f;
           const float lsum = wave_sum(e);
-          if (lane < n) p_s[h * AC + lane] = e;
-          if (lane == 0) {
-            ml[2 * h] = mx;
-            ml[2 * h + 1] = lsum;
+          float o0 = 0.f, o1 = 0.f;
+          // fully unrolled (n <= AC): the weight of position t comes from lane t
+#pragma unroll
+          for (int t = 0; t < AC; t++) {
+            const float et = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), t));
+            const float *vt = v_s + t * d;
+            if (t < n) {
+              o0 = fmaf(et, lane < d ? vt[lane] : 0.f, o0);
+              o1 = fmaf(et, lane + 64 < d ? vt[lane + 64] : 0.f, o1);
+            }
           }
-        }
-        __syncthreads();
-        for (int i = tid; i < gq * d; i += NT) {
-          const int h = i / d, j = i - h * d;
-          float o = 0.f;
-          for (int t = 0; t < n; t++) o = fmaf(p_s[h * AC + t], v_s[t * d + j], o);
           uint64_t *dst = a.tpart + ((size_t)(g * gq + h) * nchmax + c) * (d + 2);
-          tput(dst + j, o, T + P_PART);
-          if (j == 0) {
-            tput(dst + d, ml[2 * h], T + P_PART);
-            tput(dst + d + 1, ml[2 * h + 1], T + P_PART);
+          if (lane < d) tput(dst + lane, o0, T + P_PART);
+          if (lane + 64 < d) tput(dst + lane + 64, o1, T + P_PART);
+          if (lane == 0) {
+            tput(dst + d, mx, T + P_PART);
+            tput(dst + d + 1, lsum, T + P_PART);
           }
         }
         __syncthreads();
       }
 
       // ---- merge: q head h's chunks -> att[h] (tag T + P_ATT), on the last
-      // workgroups (attention items start at the first) --------------------
+      // workgroups (attention items start at the first); one wave combines
+      // att = sum_c e^(m_c - M) o_c / sum_c e^(m_c - M) l_c ----------------
       const int mh = NB - 1 - wg;
       if (mh < a.nq) {
         const int dd = d + 2;
@@ -565,28 +802,29 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
         float *wc = big + nch * dd;          // [nch] chunk weights
         const int base = mh * nchmax * dd;
         tgather<2>(a.tpart, [base](int i) { return base + i; }, nch * dd, T + P_PART, pc, a, &fail_s);
-        if (tid == 0) {
-          // w_c = e^(m_c - M) / sum_c e^(m_c - M) l_c
-          float mx = -INFINITY;
-          for (int c = 0; c < nch; c++) mx = fmaxf(mx, pc[c * dd + d]);
-          float lsum = 0.f;
-          for (int c = 0; c < nch; c++) {
+        if (wave == 0) {
+          float mloc = -INFINITY;
+          for (int c = lane; c < nch; c += 64) mloc = fmaxf(mloc, pc[c * dd + d]);
+          const float mx = wave_max(mloc);
+          float lloc = 0.f;
+          for (int c = lane; c < nch; c += 64) {
             const float e = expf(pc[c * dd + d] - mx);
             wc[c] = e;
-            lsum = fmaf(e, pc[c * dd + d + 1], lsum);
+            lloc = fmaf(e, pc[c * dd + d + 1], lloc);
           }
-          const float inv = 1.0f / lsum;
-          for (int c = 0; c < nch; c++) wc[c] *= inv;
-        }
-        __syncthreads();
-        for (int j = tid; j < d; j += NT) {
-          float acc = 0.f;
-          for (int c = 0; c < nch; c++) acc = fmaf(wc[c], pc[c * dd + j], acc);
-          tput(a.tatt + mh * d + j, acc, T + P_ATT);
+          const float inv = 1.0f / wave_sum(lloc);
+          for (int j = lane; j < d; j += 64) {
+            float acc = 0.f;
+#pragma unroll 4
+            for (int c = 0; c < nch; c++) acc = fmaf(wc[c], pc[c * dd + j], acc);
+            tput(a.tatt + mh * d + j, acc * inv, T + P_ATT);
+          }
         }
         __syncthreads();
       }
       mark(a, s, 2 + 5 * l);
+      issue_o(l, true);
+      issue_gu(l, true, 2);
 
       // ---- o projection + residual (tag T + P_XO) -----------------------------
       tgather_lin<3>(a.tatt, qdim, T + P_ATT, att, a, &fail_s);
@@ -598,42 +836,36 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
           tput(a.txo + xrow, xl[wave], T + P_XO);
         }
       }
+      issue_gu(l, true, 3);
+      issue_gu(l, true, 4);
+      issue_down(l, true, 2);
 
       // ---- gate/up + SwiGLU (tag T + P_H) -------------------------------------
-      // pairs 0 and 1 load while X_o is awaited; pair p + 2 loads while p computes
-      ldrow<HC>(gA0, L.wgu, H, gu_row(0), gu_row(0) < g1, lane);
-      ldrow<HC>(gA1, L.wgu, H, gu_row(0) + 1, gu_row(0) < g1, lane);
-      ldrow<HC>(gB0, L.wgu, H, gu_row(1), gu_row(1) < g1, lane);
-      ldrow<HC>(gB1, L.wgu, H, gu_row(1) + 1, gu_row(1) < g1, lane);
+      load_gw<HC>(gw, L.ln2, H, lane);
       tgather_lin<3>(a.txo, H, T + P_XO, xs, a, &fail_s);
       mark(a, s, 4 + 5 * l);
-      rmsnorm_lds(xs, L.ln2, H, a.eps, red);
+      // every dot first, then the stores
+      float gy[GPMAX][2];
+      {
+        float4 xr[HC][2];
+        XPairs<HC> xp;
+        norm_x<HC>(xr, xp, xs, gw, H, a.eps, lane);
+#pragma unroll
+        for (int p = 0; p < GPMAX; p++) {
+          gy[p][0] = gu_row(p) < g1 ? dotrow_p<HC>(gu[p][0], xp) : 0.f;
+          gy[p][1] = gu_row(p) < g1 ? dotrow_p<HC>(gu[p][1], xp) : 0.f;
+        }
+      }
 #pragma unroll
       for (int p = 0; p < GPMAX; p++) {
-        const int row = gu_row(p), nrow = gu_row(p + 2);
-        const bool nv2 = p + 2 < GPMAX && nrow < g1;
-        float y0 = 0.f, y1 = 0.f;
-        if (p % 2 == 0) {
-          if (row < g1) {
-            y0 = dotrow<HC>(gA0, xs, H, lane);
-            y1 = dotrow<HC>(gA1, xs, H, lane);
-          }
-          ldrow<HC>(gA0, L.wgu, H, nrow, nv2, lane);
-          ldrow<HC>(gA1, L.wgu, H, nrow + 1, nv2, lane);
-        } else {
-          if (row < g1) {
-            y0 = dotrow<HC>(gB0, xs, H, lane);
-            y1 = dotrow<HC>(gB1, xs, H, lane);
-          }
-          ldrow<HC>(gB0, L.wgu, H, nrow, nv2, lane);
-          ldrow<HC>(gB1, L.wgu, H, nrow + 1, nv2, lane);
-        }
-        if (row < g1 && lane == 0) tput(a.th + (row >> 1), silu(y0) * y1, T + P_H);
+        const int row = gu_row(p);
+        if (row < g1 && lane == 0) tput(a.th + (row >> 1), silu(gy[p][0]) * gy[p][1], T + P_H);
       }
-      // next weights: down of this layer, QKV and o of the next layer
-      uint8_t *wd_s = wdl + (size_t)wave * I * 2;
-      dma_row(L.wd, I, xrow, has_x, wd_s, lane);
-      if (l + 1 < a.L) issue_qo(l + 1);
+      if (l + 1 < a.L) {
+        issue_q(l + 1, true);
+        issue_gu(l + 1, true, 0);
+        issue_gu(l + 1, true, 1);
+      }
 
       // ---- down + residual (tag T + P_XD) -------------------------------------
       tgather_lin<18>(a.th, I, T + P_H, big, a, &fail_s);
@@ -645,32 +877,50 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
           tput(a.txd + xrow, xl[wave], T + P_XD);
         }
       }
+      if (l + 1 < a.L) {
+        issue_down(l + 1, true, 0);
+        issue_down(l + 1, true, 1);
+      }
     }
 
     // ---- final norm + head + argmax partial (tag tstep + 5L) -----------------
     const uint32_t TH = tstep + (uint32_t)a.L * kTPL;
-    tgather_lin<3>(a.txd, H, TH - kTPL + P_XD, xs, a, &fail_s);
-    mark(a, s, 1 + 5 * a.L);
-    rmsnorm_lds(xs, a.final_norm, H, a.eps, red);
-    if (wg == 0)
-      for (int j = tid; j < H; j += NT) a.normed[j] = xs[j];
     float bv = -INFINITY;
     uint32_t bi = 0xffffffffu;
     {
+      XPairs<HC> xp;
+      {
+        u32x4 gw[HC];
+        load_gw<HC>(gw, a.final_norm, H, lane);
+        tgather_lin<3>(a.txd, H, TH - kTPL + P_XD, xs, a, &fail_s);
+        mark(a, s, 1 + 5 * a.L);
+        float4 xr[HC][2];
+        norm_x<HC>(xr, xp, xs, gw, H, a.eps, lane);
+        if (wg == 0 && wave == 0) {
+#pragma unroll
+          for (int i = 0; i < HC; i++) {
+            const int c = lane + i * 64;
+            if (c < (H >> 3)) {
+              *(float4 *)(a.normed + c * 8) = xr[i][0];
+              *(float4 *)(a.normed + c * 8 + 4) = xr[i][1];
+            }
+          }
+        }
+      }
       // this wave's rows v0 + wave*HT + k*NW*HT, two tiles in flight
       u32x4 ta[HT][HC], tb[HT][HC];
       const int stride = NW * HT;
       int r0 = v0 + wave * HT;
 #pragma unroll
-      for (int r = 0; r < HT; r++) ldrow<HC>(ta[r], a.head, H, r0 + r, r0 + r < v1, lane);
+      for (int r = 0; r < HT; r++) ldrow_all<HC>(ta[r], a.head, H, r0 + r, v1 - 1, lane);
       for (; r0 < v1; r0 += 2 * stride) {
         const int r1 = r0 + stride;
 #pragma unroll
-        for (int r = 0; r < HT; r++) ldrow<HC>(tb[r], a.head, H, r1 + r, r1 + r < v1, lane);
+        for (int r = 0; r < HT; r++) ldrow_all<HC>(tb[r], a.head, H, r1 + r, v1 - 1, lane);
 #pragma unroll
         for (int r = 0; r < HT; r++)
           if (r0 + r < v1) {
-            const float y = dotrow<HC>(ta[r], xs, H, lane);
+            const float y = dotrow_p<HC>(ta[r], xp);
             if (lane == 0) a.logits[r0 + r] = y;
             if (beats(y, (uint32_t)(r0 + r), bv, bi)) {
               bv = y;
@@ -679,11 +929,11 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
           }
         const int r2 = r1 + stride;
 #pragma unroll
-        for (int r = 0; r < HT; r++) ldrow<HC>(ta[r], a.head, H, r2 + r, r2 + r < v1, lane);
+        for (int r = 0; r < HT; r++) ldrow_all<HC>(ta[r], a.head, H, r2 + r, v1 - 1, lane);
 #pragma unroll
         for (int r = 0; r < HT; r++)
           if (r1 + r < v1) {
-            const float y = dotrow<HC>(tb[r], xs, H, lane);
+            const float y = dotrow_p<HC>(tb[r], xp);
             if (lane == 0) a.logits[r1 + r] = y;
             if (beats(y, (uint32_t)(r1 + r), bv, bi)) {
               bv = y;
@@ -692,7 +942,7 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
           }
       }
     }
-    if (s + 1 < a.steps) issue_qo(0);
+    if (s + 1 < a.steps) issue_first(0);
     if (lane == 0) best_s[wave] = make_float2(bv, __uint_as_float(bi));
     __syncthreads();
     if (tid == 0) {
@@ -757,7 +1007,8 @@ size_t persist_part_words(int nq, int max_seq, int d) {
 bool persist_supported(int H, int I, int qdim, int d, int gq) {
   if (H % 8 || I % 8 || qdim % 8) return false;
   if (H > MAXH || qdim > MAXH || I > MAXI) return false;
-  if (d % 8 || d > MAXD || gq > 8) return false;
+  // the attention items sum a score over d / 4 lanes: d in {32, 64, 128}
+  if ((d & (d - 1)) || d < 32 || d > MAXD || gq > 8) return false;
   // each workgroup's gate/up pairs fit GPMAX per wavefront, residual rows and
   // QKV pairs one per wavefront
   const int gper = (((2 * I + NB - 1) / NB) + 1) & ~1;
