@@ -361,10 +361,11 @@ __device__ __forceinline__ float dot2(uint32_t w, uint32_t x, float acc) {
   return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w), __builtin_bit_cast(bf16x2, x),
                                          acc, false);
 }
-// f32 -> bf16 bits, round to nearest even (finite inputs)
-__device__ __forceinline__ uint32_t bf16_rne(float f) {
-  const uint32_t u = __float_as_uint(f);
-  return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+// (a, b) -> bf16 pair (a low, b high), round to nearest even: one v_cvt_pk_bf16_f32
+__device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
+  const f32x2 f = {a, b};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2));
 }
 // This lane's chunks of x (chunk lane + 64 i, 8 columns each) as bf16 pairs
 // x = hi + lo: hi is x rounded to bf16, lo the remainder rounded to bf16, so
@@ -403,11 +404,9 @@ __device__ __forceinline__ void norm_x(float4 (&xr)[C][2], XPairs<C> &xp, const 
       const float a = bf_lo(g[j]) * (v[2 * j] * inv), b = bf_hi(g[j]) * (v[2 * j + 1] * inv);
       v[2 * j] = a;
       v[2 * j + 1] = b;
-      const uint32_t ha = bf16_rne(a), hb = bf16_rne(b);
-      const uint32_t la = bf16_rne(a - __uint_as_float(ha << 16));
-      const uint32_t lb = bf16_rne(b - __uint_as_float(hb << 16));
-      xp.h[i][j] = ha | (hb << 16);
-      xp.l[i][j] = la | (lb << 16);
+      const uint32_t hp = pack_bf16(a, b);
+      xp.h[i][j] = hp;
+      xp.l[i][j] = pack_bf16(a - bf_lo(hp), b - bf_hi(hp));
     }
     xr[i][0] = make_float4(v[0], v[1], v[2], v[3]);
     xr[i][1] = make_float4(v[4], v[5], v[6], v[7]);
@@ -463,6 +462,11 @@ __device__ __forceinline__ void mark(const PersistArgs &a, uint32_t s, int slot)
     a.trace[(size_t)blockIdx.x * (5 * a.L + 3) + slot] = wall_clock64();
 }
 
+// Every dimension of the model is a template constant, or 0 to read it from
+// the launch arguments: the launcher picks the Qwen2.5-1.5B instantiation for
+// that shape, where folding the dimensions frees the scalar registers that
+// the generic build would spill, and the generic one for every other shape.
+template <int kH, int kI, int kV, int kNQ, int kNKV, int kD>
 __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
   extern __shared__ float4 sm4[];
   float *xs = (float *)sm4;     // [MAXH] activation for the current phase
@@ -480,19 +484,21 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
   int tid = threadIdx.x, lane = tid & 63;
   const int wg = blockIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int H = a.H, I = a.I, d = a.d, half = d >> 1, gq = a.nq / a.nkv;
-  const int qdim = a.nq * d, kvdim = a.nkv * d;
+  const int H = kH ? kH : a.H, I = kI ? kI : a.I, V = kV ? kV : a.V, d = kD ? kD : a.d;
+  const int nq = kNQ ? kNQ : a.nq, nkv = kNKV ? kNKV : a.nkv;
+  const int half = d >> 1, gq = nq / nkv;
+  const int qdim = nq * d, kvdim = nkv * d, qkv_rows = qdim + 2 * kvdim;
   const uint32_t TPS = (uint32_t)a.L * kTPL + 2;
   const int nchmax = (a.max_seq + AC - 1) / AC;
   // ownership
-  const int qper = (((a.qkv_rows + NB - 1) / NB) + 1) & ~1;
-  const int q0 = wg * qper, q1 = min(q0 + qper, a.qkv_rows);
+  const int qper = (((qkv_rows + NB - 1) / NB) + 1) & ~1;
+  const int q0 = wg * qper, q1 = min(q0 + qper, qkv_rows);
   const int xper = (H + NB - 1) / NB;
   const int x0 = wg * xper, x1 = min(x0 + xper, H);
   const int gper = (((2 * I + NB - 1) / NB) + 1) & ~1;
   const int g0 = wg * gper, g1 = min(g0 + gper, 2 * I);
-  const int vper = (a.V + NB - 1) / NB;
-  const int v0 = wg * vper, v1 = min(v0 + vper, a.V);
+  const int vper = (V + NB - 1) / NB;
+  const int v0 = wg * vper, v1 = min(v0 + vper, V);
   const int qrow = q0 + 2 * wave;      // this wave's QKV pair
   const int xrow = x0 + wave;          // this wave's residual row (o and down)
   const bool has_q = qrow < q1, has_x = xrow < x1;
@@ -591,7 +597,7 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
           if (beats(best_s[w].x, __float_as_uint(best_s[w].y), b.x, __float_as_uint(b.y)))
             b = best_s[w];
         const uint32_t idx = __float_as_uint(b.y);
-        tok_s = idx < (uint32_t)a.V ? idx : 0u;  // no candidate (all NaN / -inf) -> 0
+        tok_s = idx < (uint32_t)V ? idx : 0u;  // no candidate (all NaN / -inf) -> 0
         if (wg == 0) a.out_ids[s] = tok_s;
       }
       __syncthreads();
@@ -669,8 +675,8 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
       // then wave h takes q head h: softmax over the chunk in its lanes and
       // the V sum with each weight read back from the lane that holds it.
       const int nch = (seq + AC - 1) / AC;
-      for (int it = wg; it < a.nkv * nch; it += NB) {
-        const int g = it % a.nkv, c = it / a.nkv;
+      for (int it = wg; it < nkv * nch; it += NB) {
+        const int g = it % nkv, c = it / nkv;
         const int t0 = c * AC, n = min(AC, seq - t0);
         const bool has_cur = (int)pos < t0 + n;  // this step's row ends the chunk
         const int nold = has_cur ? n - 1 : n;
@@ -771,14 +777,16 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
           const float e = lane < n ? expf(sc - mx) : 0.f;
           const float lsum = wave_sum(e);
           float o0 = 0.f, o1 = 0.f;
-          // fully unrolled (n <= AC): the weight of position t comes from lane t
+          // fully unrolled (n <= AC): the weight of position t comes from lane
+          // t; lanes past the head's columns read in-row duplicates and drop them
+          const int j0 = lane & (d - 1), j1 = (lane + 64) & (d - 1);
 #pragma unroll
           for (int t = 0; t < AC; t++) {
             const float et = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), t));
             const float *vt = v_s + t * d;
             if (t < n) {
-              o0 = fmaf(et, lane < d ? vt[lane] : 0.f, o0);
-              o1 = fmaf(et, lane + 64 < d ? vt[lane + 64] : 0.f, o1);
+              o0 = fmaf(et, vt[j0], o0);
+              o1 = fmaf(et, vt[j1], o1);
             }
           }
           uint64_t *dst = a.tpart + ((size_t)(g * gq + h) * nchmax + c) * (d + 2);
@@ -796,7 +804,7 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
       // workgroups (attention items start at the first); one wave combines
       // att = sum_c e^(m_c - M) o_c / sum_c e^(m_c - M) l_c ----------------
       const int mh = NB - 1 - wg;
-      if (mh < a.nq) {
+      if (mh < nq) {
         const int dd = d + 2;
         float *pc = big;                     // [nch][d + 2] gathered partials
         float *wc = big + nch * dd;          // [nch] chunk weights
@@ -1054,16 +1062,18 @@ hipError_t launch_decode_persistent(const PersistArgs &a, hipStream_t s) {
   PersistArgs args = a;
   const size_t smem = persist_lds(args);
   if (smem > kMaxLds) return hipErrorInvalidValue;
-  static bool attr_set = false;
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute((const void *)decode_persistent_kernel,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxLds);
+  const bool qwen15 = a.H == 1536 && a.I == 8960 && a.V == 151936 && a.nq == 12 && a.nkv == 2 &&
+                      a.d == 128;
+  const void *fn = qwen15 ? (const void *)decode_persistent_kernel<1536, 8960, 151936, 12, 2, 128>
+                          : (const void *)decode_persistent_kernel<0, 0, 0, 0, 0, 0>;
+  static bool attr_set[2] = {false, false};
+  if (!attr_set[qwen15]) {
+    hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxLds);
     if (e != hipSuccess) return e;
-    attr_set = true;
+    attr_set[qwen15] = true;
   }
   void *params[] = {&args};
-  return hipLaunchCooperativeKernel((const void *)decode_persistent_kernel, dim3(NB), dim3(NT),
-                                    params, (unsigned)smem, s);
+  return hipLaunchCooperativeKernel(fn, dim3(NB), dim3(NT), params, (unsigned)smem, s);
 }
 
 }  // namespace myos
