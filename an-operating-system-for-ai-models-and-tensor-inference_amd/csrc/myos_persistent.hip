@@ -152,6 +152,10 @@ struct Linear {
 // tgather for src[0, n) in order: one buffer descriptor, one lane offset and
 // per-unroll constant offsets keep the address cost at one register. The
 // loads are sc1 (device-coherent) and volatile, so a spin re-reads memory.
+// A wait that starts before its producers have published would otherwise
+// re-read all U words per spin from every workgroup at once, which costs
+// bandwidth the weight stream needs: each thread first spins on its last
+// word alone, then reads the rest once, re-reading only words still untagged.
 template <int U>
 __device__ bool tgather_lin(const uint64_t *src, int n, uint32_t tag, float *dst,
                             const PersistArgs &a, int *fail) {
@@ -160,20 +164,34 @@ __device__ bool tgather_lin(const uint64_t *src, int n, uint32_t tag, float *dst
       __builtin_amdgcn_make_buffer_rsrc((void *)src, (short)0, n * 8, 0x00020000);
   bool ok = *fail == 0;
   for (int i0 = threadIdx.x; i0 < n && ok; i0 += NT * U) {
-    uint64_t w[U];
+    const int last = min(U - 1, (n - 1 - i0) / NT);
     for (unsigned spins = 0;; spins++) {
+      const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(rs, (i0 + last * NT) * 8, 0, kAux);
+      if (v.y == tag) break;
+      if (spin_fail(a, spins)) {
+        ok = false;
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+    }
+    uint64_t w[U];
+    uint32_t pend = 0;
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      w[u] = (uint64_t)tag << 32;
+      if (i0 + u * NT < n) pend |= 1u << u;
+    }
+    for (unsigned spins = 0; ok; spins++) {
 #pragma unroll
       for (int u = 0; u < U; u++)
-        if (i0 + u * NT < n) {
+        if (pend & (1u << u)) {
           const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(rs, i0 * 8, u * NT * 8, kAux);
           w[u] = ((uint64_t)v.y << 32) | v.x;
-        } else {
-          w[u] = (uint64_t)tag << 32;
         }
-      bool ready = true;
 #pragma unroll
-      for (int u = 0; u < U; u++) ready = ready && (uint32_t)(w[u] >> 32) == tag;
-      if (ready) break;
+      for (int u = 0; u < U; u++)
+        if ((uint32_t)(w[u] >> 32) == tag) pend &= ~(1u << u);
+      if (!pend) break;
       if (spin_fail(a, spins)) {
         ok = false;
         break;
@@ -495,8 +513,18 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
   const int q0 = wg * qper, q1 = min(q0 + qper, qkv_rows);
   const int xper = (H + NB - 1) / NB;
   const int x0 = wg * xper, x1 = min(x0 + xper, H);
-  const int gper = (((2 * I + NB - 1) / NB) + 1) & ~1;
-  const int g0 = wg * gper, g1 = min(g0 + gper, 2 * I);
+  // Gate/up pairs go to the workgroups that run no attention item (the
+  // first nkv * nchmax) and no merge (the last nq) when those can hold them:
+  // the attention chain's workgroups then carry almost no weight loads into
+  // their waits. Otherwise every workgroup takes a share.
+  int gst = nkv * nchmax, gen = NB - nq;
+  if (gen - gst <= 0 || (gen - gst) * GPMAX * NW < I) {
+    gst = 0;
+    gen = NB;
+  }
+  const int gper = 2 * ((I + (gen - gst) - 1) / (gen - gst));
+  const int g0 = wg >= gst && wg < gen ? (wg - gst) * gper : 2 * I;
+  const int g1 = min(g0 + gper, 2 * I);
   const int vper = (V + NB - 1) / NB;
   const int v0 = wg * vper, v1 = min(v0 + vper, V);
   const int qrow = q0 + 2 * wave;      // this wave's QKV pair
@@ -508,20 +536,18 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
   __syncthreads();
 
   // Weight rows held on chip across phases: this wave's QKV pair, o row and
-  // gate/up pairs in registers, its down row in LDS. Loads run up to a layer
-  // ahead of their use, spread over the four waits of a layer (h, x,
-  // attention, X_o) so that HBM streams through the whole dependency chain:
-  //   after gate/up(l):  QKV(l+1), gate/up slots 0, 1 of l+1
-  //   after down(l):     down parts 0, 1 of l+1
-  //   after merge(l):    o(l), gate/up slot 2 of l
-  //   after o(l):        gate/up slots 3, 4 of l, down part 2 of l
-  // Layer 0's first share loads after the head instead, so that no weight
-  // row is live across the head's own tiles; the attention items (the other
-  // register peak) see only slots 0 and 1 live.
-  // Each wait re-polls with vector loads, so it also waits for every load
-  // issued before it, and a wave that issues more loads than the CU's memory
-  // queue holds stalls at the issue itself: each wait gets about a quarter
-  // of the layer's bytes, issued after the phase's arithmetic.
+  // gate/up pairs in registers, its down row in LDS. A wait re-polls with
+  // vector loads, which queue behind every load the CU issued before them,
+  // so loads go out right after a wait returns and drain while the next
+  // phase computes, each batch as soon as its registers are free:
+  //   after the items of l (before the merge): o(l), gate/up slots 2-4 of l
+  //   after the attention wait of l:           QKV(l+1)
+  //   after the h wait of l:                   gate/up slots 0, 1 of l+1
+  // Loads into LDS make the compiler wait for them before the wave's next
+  // LDS access, so the down row goes just before a wait instead:
+  //   after o(l): part 2 of l;   after down(l): parts 0, 1 of l+1
+  // Layer 0's first share loads after the head, so that no weight row is
+  // live across the head's own tiles.
   u32x4 wq0[HC], wq1[HC], wo[HC];
   u32x4 gu[GPMAX][2][HC];  // gate/up slot p: rows (2i, 2i+1) = (gate_i, up_i)
   uint8_t *wd_s = wdl + (size_t)wave * I * 2;  // this wave's down row
@@ -800,6 +826,11 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
         __syncthreads();
       }
 
+      issue_o(l, true);
+      issue_gu(l, true, 2);
+      issue_gu(l, true, 3);
+      issue_gu(l, true, 4);
+
       // ---- merge: q head h's chunks -> att[h] (tag T + P_ATT), on the last
       // workgroups (attention items start at the first); one wave combines
       // att = sum_c e^(m_c - M) o_c / sum_c e^(m_c - M) l_c ----------------
@@ -831,12 +862,11 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
         __syncthreads();
       }
       mark(a, s, 2 + 5 * l);
-      issue_o(l, true);
-      issue_gu(l, true, 2);
 
       // ---- o projection + residual (tag T + P_XO) -----------------------------
       tgather_lin<3>(a.tatt, qdim, T + P_ATT, att, a, &fail_s);
       mark(a, s, 3 + 5 * l);
+      if (l + 1 < a.L) issue_q(l + 1, true);
       if (has_x) {
         const float y = dotrow<HC>(wo, att, qdim, lane);
         if (lane == 0) {
@@ -844,8 +874,6 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
           tput(a.txo + xrow, xl[wave], T + P_XO);
         }
       }
-      issue_gu(l, true, 3);
-      issue_gu(l, true, 4);
       issue_down(l, true, 2);
 
       // ---- gate/up + SwiGLU (tag T + P_H) -------------------------------------
@@ -869,15 +897,15 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
         const int row = gu_row(p);
         if (row < g1 && lane == 0) tput(a.th + (row >> 1), silu(gy[p][0]) * gy[p][1], T + P_H);
       }
-      if (l + 1 < a.L) {
-        issue_q(l + 1, true);
-        issue_gu(l + 1, true, 0);
-        issue_gu(l + 1, true, 1);
-      }
+
 
       // ---- down + residual (tag T + P_XD) -------------------------------------
       tgather_lin<18>(a.th, I, T + P_H, big, a, &fail_s);
       mark(a, s, 5 + 5 * l);
+      if (l + 1 < a.L) {
+        issue_gu(l + 1, true, 0);
+        issue_gu(l + 1, true, 1);
+      }
       if (has_x) {
         const float y = dotrow_lds(wd_s, big, I, lane);
         if (lane == 0) {
