@@ -464,6 +464,16 @@ __device__ __forceinline__ float dotrow_p(const u32x4 (&t)[C], const XPairs<C> &
 
 __device__ __forceinline__ float silu(float z) { return z / (1.0f + expf(-z)); }
 
+// A pointer read from LDS, made provably wave-uniform: kept in scalar
+// registers, so a buffer descriptor built from it needs no per-lane loop.
+template <class T>
+__device__ __forceinline__ T *uni(T *p) {
+  const uint64_t v = (uint64_t)p;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return (T *)(((uint64_t)hi << 32) | lo);
+}
+
 // The value itself, through an empty volatile asm: the compiler cannot treat
 // it (or anything computed from it) as loop-invariant.
 __device__ __forceinline__ int opaque(int v) {
@@ -531,6 +541,12 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
   const int xrow = x0 + wave;          // this wave's residual row (o and down)
   const bool has_q = qrow < q1, has_x = xrow < x1;
 
+  // The layer table, copied to LDS once: a weight pointer read from global
+  // memory inside the loop would be a vector load whose wait (vmcnt 0) also
+  // waits for every weight load in flight.
+  PersistLayer *lay = (PersistLayer *)(wdl + (size_t)xper * I * 2);
+  for (int i = tid; i < a.L * (int)(sizeof(PersistLayer) / 8); i += NT)
+    ((uint64_t *)lay)[i] = ((const uint64_t *)a.layers)[i];
   if (tid == 0) fail_s = 0;
   if (tid < NW) xl[tid] = 0.f;
   __syncthreads();
@@ -540,11 +556,13 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
   // vector loads, which queue behind every load the CU issued before them,
   // so loads go out right after a wait returns and drain while the next
   // phase computes, each batch as soon as its registers are free:
-  //   after the items of l (before the merge): o(l), gate/up slots 2-4 of l
+  //   after the items of l (before the merge): o(l), gate/up slots 1-4 of l
   //   after the attention wait of l:           QKV(l+1)
-  //   after the h wait of l:                   gate/up slots 0, 1 of l+1
-  // Loads into LDS make the compiler wait for them before the wave's next
-  // LDS access, so the down row goes just before a wait instead:
+  //   during gate/up(l), after slot 0's dots:  gate/up slot 0 of l+1
+  // A wave that issues more loads than its memory queue holds stalls at the
+  // issue, so big batches go out where the wave would wait anyway. Loads into
+  // LDS make the compiler wait for them before the wave's next LDS access,
+  // so the down row goes just before a wait:
   //   after o(l): part 2 of l;   after down(l): parts 0, 1 of l+1
   // Layer 0's first share loads after the head, so that no weight row is
   // live across the head's own tiles.
@@ -555,25 +573,25 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
   // gate/up pair in slot p of this wavefront
   auto gu_row = [&](int p) { return g0 + 2 * (wave + p * NW); };
   auto issue_q = [&](int l, bool v) {
-    const PersistLayer &L = a.layers[l];
-    ldrow<HC>(wq0, L.wqkv, H, qrow, v && has_q, lane);
-    ldrow<HC>(wq1, L.wqkv, H, qrow + 1, v && has_q, lane);
+    const uint16_t *w = uni(lay[l].wqkv);
+    ldrow<HC>(wq0, w, H, qrow, v && has_q, lane);
+    ldrow<HC>(wq1, w, H, qrow + 1, v && has_q, lane);
   };
-  auto issue_o = [&](int l, bool v) { ldrow<HC>(wo, a.layers[l].wo, qdim, xrow, v && has_x, lane); };
+  auto issue_o = [&](int l, bool v) { ldrow<HC>(wo, uni(lay[l].wo), qdim, xrow, v && has_x, lane); };
   auto issue_gu = [&](int l, bool v, int p) {
     const int row = gu_row(p);
     const bool ok = v && row < g1;
-    ldrow<HC>(gu[p][0], a.layers[l].wgu, H, row, ok, lane);
-    ldrow<HC>(gu[p][1], a.layers[l].wgu, H, row + 1, ok, lane);
+    const uint16_t *w = uni(lay[l].wgu);
+    ldrow<HC>(gu[p][0], w, H, row, ok, lane);
+    ldrow<HC>(gu[p][1], w, H, row + 1, ok, lane);
   };
   auto issue_down = [&](int l, bool v, int part) {
-    if (v && has_x) dma_row_part(a.layers[l].wd, I, xrow, wd_s, lane, part, 3);
+    if (v && has_x) dma_row_part(uni(lay[l].wd), I, xrow, wd_s, lane, part, 3);
   };
   // what layer l needs loaded before its first wait
   auto issue_first = [&](int l) {
     issue_q(l, true);
     issue_gu(l, true, 0);
-    issue_gu(l, true, 1);
     issue_down(l, true, 0);
     issue_down(l, true, 1);
   };
@@ -637,22 +655,23 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
     for (int l = 0; l < a.L; l++) {
       tid = opaque(tid);
       lane = tid & 63;
-      const PersistLayer &L = a.layers[l];
+      const uint16_t *Lln1 = uni(lay[l].ln1), *Lln2 = uni(lay[l].ln2);
+      const float *Lbqkv = uni(lay[l].bqkv);
       const uint32_t T = tstep + (uint32_t)l * kTPL;
       float *kc = a.kc + (size_t)l * a.layer_kv, *vc = a.vc + (size_t)l * a.layer_kv;
 
       // ---- QKV + bias + RoPE + KV store (tag T + P_QKV) ---------------------
       // gains, bias and this pair's (cos, sin) load while x is awaited
       u32x4 gw[HC];
-      load_gw<HC>(gw, L.ln1, H, lane);
+      load_gw<HC>(gw, Lln1, H, lane);
       const bool roped = qrow < qdim + kvdim;
       const int qu = (roped && qrow >= qdim ? qrow - qdim : qrow) >> 1;
       const int qhead = qu / half, qp = qu - qhead * half;
       float qb0 = 0.f, qb1 = 0.f;
       float2 qcs = make_float2(1.f, 0.f);
       if (has_q) {
-        qb0 = L.bqkv[qrow];
-        qb1 = L.bqkv[qrow + 1];
+        qb0 = Lbqkv[qrow];
+        qb1 = Lbqkv[qrow + 1];
         if (roped) qcs = a.rope[(size_t)pos * half + qp];
       }
       if (l > 0) tgather_lin<3>(a.txd, H, T - kTPL + P_XD, xs, a, &fail_s);
@@ -802,17 +821,25 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
           const float mx = wave_max(sc);
           const float e = lane < n ? expf(sc - mx) : 0.f;
           const float lsum = wave_sum(e);
-          float o0 = 0.f, o1 = 0.f;
-          // fully unrolled (n <= AC): the weight of position t comes from lane
-          // t; lanes past the head's columns read in-row duplicates and drop them
+          // the weights go back through LDS and are read four at a time as
+          // broadcasts; lanes past the head's columns read in-row duplicates
+          // and drop them
+          if (lane < AC) p_s[h * AC + lane] = e;
           const int j0 = lane & (d - 1), j1 = (lane + 64) & (d - 1);
+          float o0 = 0.f, o1 = 0.f;
 #pragma unroll
-          for (int t = 0; t < AC; t++) {
-            const float et = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), t));
-            const float *vt = v_s + t * d;
-            if (t < n) {
-              o0 = fmaf(et, vt[j0], o0);
-              o1 = fmaf(et, vt[j1], o1);
+          for (int t4 = 0; t4 < AC; t4 += 4) {
+            if (t4 < n) {
+              const float4 e4 = *(const float4 *)(p_s + h * AC + t4);
+              const float ev[4] = {e4.x, e4.y, e4.z, e4.w};
+#pragma unroll
+              for (int k = 0; k < 4; k++) {
+                // rows past n hold stale LDS: masked, not just weighted by 0
+                const float *vt = v_s + (t4 + k) * d;
+                const bool in = t4 + k < n;
+                o0 = fmaf(ev[k], in ? vt[j0] : 0.f, o0);
+                o1 = fmaf(ev[k], in ? vt[j1] : 0.f, o1);
+              }
             }
           }
           uint64_t *dst = a.tpart + ((size_t)(g * gq + h) * nchmax + c) * (d + 2);
@@ -827,6 +854,7 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
       }
 
       issue_o(l, true);
+      issue_gu(l, true, 1);
       issue_gu(l, true, 2);
       issue_gu(l, true, 3);
       issue_gu(l, true, 4);
@@ -877,7 +905,7 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
       issue_down(l, true, 2);
 
       // ---- gate/up + SwiGLU (tag T + P_H) -------------------------------------
-      load_gw<HC>(gw, L.ln2, H, lane);
+      load_gw<HC>(gw, Lln2, H, lane);
       tgather_lin<3>(a.txo, H, T + P_XO, xs, a, &fail_s);
       mark(a, s, 4 + 5 * l);
       // every dot first, then the stores
@@ -890,6 +918,7 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
         for (int p = 0; p < GPMAX; p++) {
           gy[p][0] = gu_row(p) < g1 ? dotrow_p<HC>(gu[p][0], xp) : 0.f;
           gy[p][1] = gu_row(p) < g1 ? dotrow_p<HC>(gu[p][1], xp) : 0.f;
+          if (p == 0 && l + 1 < a.L) issue_gu(l + 1, true, 0);
         }
       }
 #pragma unroll
@@ -902,10 +931,7 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
       // ---- down + residual (tag T + P_XD) -------------------------------------
       tgather_lin<18>(a.th, I, T + P_H, big, a, &fail_s);
       mark(a, s, 5 + 5 * l);
-      if (l + 1 < a.L) {
-        issue_gu(l + 1, true, 0);
-        issue_gu(l + 1, true, 1);
-      }
+
       if (has_x) {
         const float y = dotrow_lds(wd_s, big, I, lane);
         if (lane == 0) {
@@ -917,6 +943,7 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
         issue_down(l + 1, true, 0);
         issue_down(l + 1, true, 1);
       }
+
     }
 
     // ---- final norm + head + argmax partial (tag tstep + 5L) -----------------
@@ -1069,7 +1096,7 @@ static size_t persist_lds(PersistArgs &a) {
   const size_t wd_off = 2 * MAXH + ((big + 3) & ~(size_t)3);  // floats
   const size_t xper = (size_t)(a.H + NB - 1) / NB;
   a.lds_wd = (int)wd_off;
-  return wd_off * sizeof(float) + xper * (size_t)a.I * 2;
+  return wd_off * sizeof(float) + xper * (size_t)a.I * 2 + (size_t)a.L * sizeof(PersistLayer);
 }
 
 bool persist_device_ok(const PersistArgs &a) {
