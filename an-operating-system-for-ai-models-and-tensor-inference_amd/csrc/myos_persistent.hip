@@ -156,9 +156,9 @@ struct Linear {
 // re-read all U words per spin from every workgroup at once, which costs
 // bandwidth the weight stream needs: each thread first spins on its last
 // word alone, then reads the rest once, re-reading only words still untagged.
-template <int U>
-__device__ bool tgather_lin(const uint64_t *src, int n, uint32_t tag, float *dst,
-                            const PersistArgs &a, int *fail) {
+template <int U, class Put>
+__device__ bool tgather_lin_to(const uint64_t *src, int n, uint32_t tag, Put put,
+                               const PersistArgs &a, int *fail) {
   constexpr int kAux = 16 | (1 << 31);  // sc1, volatile
   const __amdgpu_buffer_rsrc_t rs =
       __builtin_amdgcn_make_buffer_rsrc((void *)src, (short)0, n * 8, 0x00020000);
@@ -201,12 +201,18 @@ __device__ bool tgather_lin(const uint64_t *src, int n, uint32_t tag, float *dst
 #pragma unroll
     for (int u = 0; u < U; u++) {
       const int i = i0 + u * NT;
-      if (i < n) dst[i] = __uint_as_float((uint32_t)w[u]);
+      if (i < n) put(i, __uint_as_float((uint32_t)w[u]));
     }
   }
   if (!ok) *fail = 1;
   __syncthreads();
   return *fail == 0;
+}
+
+template <int U>
+__device__ bool tgather_lin(const uint64_t *src, int n, uint32_t tag, float *dst,
+                            const PersistArgs &a, int *fail) {
+  return tgather_lin_to<U>(src, n, tag, [dst](int i, float v) { dst[i] = v; }, a, fail);
 }
 
 // ---- row tiles -----------------------------------------------------------------
@@ -272,26 +278,6 @@ __device__ __forceinline__ void dma_row_part(const uint16_t *W, int k, int row, 
           rs, (__attribute__((address_space(3))) void *)(dst + i * 1024), 16, lane * 16,
           soff + i * 1024, 0, 2 /* nt */);
   }
-}
-
-// row held in LDS (16 bytes per 8-column chunk) dotted with x in LDS
-__device__ __forceinline__ float dotrow_lds(const uint8_t *wl, const float *x, int k, int lane) {
-  const int nch = k >> 3;
-  float s = 0.f;
-#pragma unroll 4
-  for (int c = lane; c < nch; c += 64) {
-    const u32x4 w = *(const u32x4 *)(wl + c * 16);
-    const float4 x0 = *(const float4 *)(x + c * 8), x1 = *(const float4 *)(x + c * 8 + 4);
-    s = fmaf(bf_lo(w.x), x0.x, s);
-    s = fmaf(bf_hi(w.x), x0.y, s);
-    s = fmaf(bf_lo(w.y), x0.z, s);
-    s = fmaf(bf_hi(w.y), x0.w, s);
-    s = fmaf(bf_lo(w.z), x1.x, s);
-    s = fmaf(bf_hi(w.z), x1.y, s);
-    s = fmaf(bf_lo(w.w), x1.z, s);
-    s = fmaf(bf_hi(w.w), x1.w, s);
-  }
-  return wave_sum(s);
 }
 
 // one row (held 8 columns per chunk per lane) dotted with x in LDS; all lanes
@@ -458,6 +444,28 @@ __device__ __forceinline__ float dotrow_p(const u32x4 (&t)[C], const XPairs<C> &
     s = dot2(w.z, xp.l[i][2], s);
     s = dot2(w.w, xp.h[i][3], s);
     s = dot2(w.w, xp.l[i][3], s);
+  }
+  return wave_sum(s);
+}
+
+// A row held in LDS (16 bytes per 8-column chunk) times x held in LDS as bf16
+// hi and lo planes (x = hi + lo, see XPairs)
+__device__ __forceinline__ float dotrow_lds_p(const uint8_t *wl, const uint16_t *xh,
+                                              const uint16_t *xl, int k, int lane) {
+  const int nch = k >> 3;
+  float s = 0.f;
+#pragma unroll 4
+  for (int c = lane; c < nch; c += 64) {
+    const u32x4 w = *(const u32x4 *)(wl + c * 16);
+    const u32x4 h = *(const u32x4 *)(xh + c * 8), l = *(const u32x4 *)(xl + c * 8);
+    s = dot2(w.x, h.x, s);
+    s = dot2(w.x, l.x, s);
+    s = dot2(w.y, h.y, s);
+    s = dot2(w.y, l.y, s);
+    s = dot2(w.z, h.z, s);
+    s = dot2(w.z, l.z, s);
+    s = dot2(w.w, h.w, s);
+    s = dot2(w.w, l.w, s);
   }
   return wave_sum(s);
 }
@@ -929,11 +937,20 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
 
 
       // ---- down + residual (tag T + P_XD) -------------------------------------
-      tgather_lin<18>(a.th, I, T + P_H, big, a, &fail_s);
+      // h lands in LDS as bf16 hi and lo planes for the down row's dot2
+      uint16_t *hh = (uint16_t *)big, *hl = hh + I;
+      tgather_lin_to<18>(
+          a.th, I, T + P_H,
+          [hh, hl](int i, float v) {
+            const uint32_t p = pack_bf16(v, 0.f);
+            hh[i] = (uint16_t)p;
+            hl[i] = (uint16_t)pack_bf16(v - bf_lo(p), 0.f);
+          },
+          a, &fail_s);
       mark(a, s, 5 + 5 * l);
 
       if (has_x) {
-        const float y = dotrow_lds(wd_s, big, I, lane);
+        const float y = dotrow_lds_p(wd_s, hh, hl, I, lane);
         if (lane == 0) {
           xl[wave] += y;
           tput(a.txd + xrow, xl[wave], T + P_XD);
