@@ -165,6 +165,7 @@ struct PersistArgs {
   uint32_t *err;
   uint32_t tag_base, steps, pos0;
   int lds_wd;                  // set by the launcher: LDS offset (floats) of the down rows
+  int kv_bf16;                 // the cache at kc / vc holds bf16 (first kernel only)
   uint64_t *trace;             // optional [grid][5 L + 3] phase timestamps of one step
   uint32_t trace_step;
 };

@@ -424,10 +424,12 @@ int setup_persistent(myos_model *m) {
   a.max_seq = (int)m->max_seq;
   a.qkv_rows = (int)m->qkv_rows;
   a.eps = s.rms_eps;
-  if (m->kv_bf16) return MYOS_OK;  // per-kernel path only
-  // MYOS_PERSIST_KERNEL=stream selects the streamed kernel (myos_stream.hip)
+  a.kv_bf16 = m->kv_bf16;
+  // MYOS_PERSIST_KERNEL=stream selects the streamed kernel (myos_stream.hip),
+  // which reads an f32 cache; a bf16 cache takes the first kernel
   const char *pk = getenv("MYOS_PERSIST_KERNEL");
   const bool want_stream = pk && std::string(pk) == "stream";
+  if (m->kv_bf16 && want_stream) return MYOS_OK;  // per-kernel path
   a.tpd = nullptr;
   m->persist_stream = want_stream && stream_device_ok(a);
   if (!m->persist_stream && !persist_device_ok(a)) return MYOS_OK;

@@ -498,11 +498,23 @@ __device__ __forceinline__ void mark(const PersistArgs &a, uint32_t s, int slot)
     a.trace[(size_t)blockIdx.x * (5 * a.L + 3) + slot] = wall_clock64();
 }
 
+// A cache value of this step (f32, or bf16 rounded to nearest even),
+// stored device-coherently.
+template <bool KB>
+__device__ __forceinline__ void kvstore(uint8_t *base, size_t idx, float v) {
+  if (KB)
+    __hip_atomic_store((uint16_t *)base + idx, (uint16_t)pack_bf16(v, 0.f), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+  else
+    cstore((float *)base + idx, v);
+}
+
 // Every dimension of the model is a template constant, or 0 to read it from
 // the launch arguments: the launcher picks the Qwen2.5-1.5B instantiation for
 // that shape, where folding the dimensions frees the scalar registers that
 // the generic build would spill, and the generic one for every other shape.
-template <int kH, int kI, int kV, int kNQ, int kNKV, int kD>
+// KB: the KV cache holds bf16 (else f32).
+template <int kH, int kI, int kV, int kNQ, int kNKV, int kD, bool KB>
 __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
   extern __shared__ float4 sm4[];
   float *xs = (float *)sm4;     // [MAXH] activation for the current phase
@@ -666,7 +678,9 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
       const uint16_t *Lln1 = uni(lay[l].ln1), *Lln2 = uni(lay[l].ln2);
       const float *Lbqkv = uni(lay[l].bqkv);
       const uint32_t T = tstep + (uint32_t)l * kTPL;
-      float *kc = a.kc + (size_t)l * a.layer_kv, *vc = a.vc + (size_t)l * a.layer_kv;
+      constexpr int kvb = KB ? 2 : 4;  // bytes per cached value
+      uint8_t *kc = (uint8_t *)a.kc + (size_t)l * a.layer_kv * kvb;
+      uint8_t *vc = (uint8_t *)a.vc + (size_t)l * a.layer_kv * kvb;
 
       // ---- QKV + bias + RoPE + KV store (tag T + P_QKV) ---------------------
       // gains, bias and this pair's (cos, sin) load while x is awaited
@@ -701,16 +715,16 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
               tput(a.tq + head * d + p + half, o1, T + P_QKV);
             } else {
               const size_t base = ((size_t)head * a.max_seq + pos) * d;
-              cstore(kc + base + p, o0);
-              cstore(kc + base + p + half, o1);
+              kvstore<KB>(kc, base + p, o0);
+              kvstore<KB>(kc, base + p + half, o1);
               tput(a.tkv + head * d + p, o0, T + P_QKV);
               tput(a.tkv + head * d + p + half, o1, T + P_QKV);
             }
           } else {
             const int rr = qrow - qdim - kvdim, head = rr / d, j = rr - head * d;
             const size_t base = ((size_t)head * a.max_seq + pos) * d + j;
-            cstore(vc + base, b0);
-            cstore(vc + base + 1, b1);
+            kvstore<KB>(vc, base, b0);
+            kvstore<KB>(vc, base + 1, b1);
             tput(a.tkv + kvdim + head * d + j, b0, T + P_QKV);
             tput(a.tkv + kvdim + head * d + j + 1, b1, T + P_QKV);
           }
@@ -741,9 +755,9 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
         // cached rows (positions < pos, complete before this step) and the
         // tagged q heads + this step's k, v of head g, all in one round trip
         const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
-            kc, (short)0, (int)(a.layer_kv * sizeof(float)), 0x00020000);
+            kc, (short)0, (int)(a.layer_kv * kvb), 0x00020000);
         const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
-            vc, (short)0, (int)(a.layer_kv * sizeof(float)), 0x00020000);
+            vc, (short)0, (int)(a.layer_kv * kvb), 0x00020000);
         u32x4 kr[KV4], vr[KV4];
 #pragma unroll
         for (int u = 0; u < KV4; u++) {
@@ -752,9 +766,16 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
           kr[u] = zero;
           vr[u] = zero;
           if (t < nold) {
-            const uint32_t off = (uint32_t)((((size_t)g * a.max_seq + t0 + t) * d + j4 * 4) * 4);
-            kr[u] = __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 16);
-            vr[u] = __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, 16);
+            const uint32_t off = (uint32_t)((((size_t)g * a.max_seq + t0 + t) * d + j4 * 4) * kvb);
+            if (KB) {  // four bf16 -> four f32 bit patterns
+              const u32x2 k2 = __builtin_amdgcn_raw_buffer_load_b64(rk, off, 0, 16);
+              const u32x2 v2 = __builtin_amdgcn_raw_buffer_load_b64(rv, off, 0, 16);
+              kr[u] = (u32x4){k2.x << 16, k2.x & 0xffff0000u, k2.y << 16, k2.y & 0xffff0000u};
+              vr[u] = (u32x4){v2.x << 16, v2.x & 0xffff0000u, v2.y << 16, v2.y & 0xffff0000u};
+            } else {
+              kr[u] = __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 16);
+              vr[u] = __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, 16);
+            }
           }
         }
         const int nqw = gq * d, nw = nqw + (has_cur ? 2 * d : 0);
@@ -1136,13 +1157,19 @@ hipError_t launch_decode_persistent(const PersistArgs &a, hipStream_t s) {
   if (smem > kMaxLds) return hipErrorInvalidValue;
   const bool qwen15 = a.H == 1536 && a.I == 8960 && a.V == 151936 && a.nq == 12 && a.nkv == 2 &&
                       a.d == 128;
-  const void *fn = qwen15 ? (const void *)decode_persistent_kernel<1536, 8960, 151936, 12, 2, 128>
-                          : (const void *)decode_persistent_kernel<0, 0, 0, 0, 0, 0>;
-  static bool attr_set[2] = {false, false};
-  if (!attr_set[qwen15]) {
+  const bool kb = a.kv_bf16 != 0;
+  const void *const fns[4] = {
+      (const void *)decode_persistent_kernel<0, 0, 0, 0, 0, 0, false>,
+      (const void *)decode_persistent_kernel<0, 0, 0, 0, 0, 0, true>,
+      (const void *)decode_persistent_kernel<1536, 8960, 151936, 12, 2, 128, false>,
+      (const void *)decode_persistent_kernel<1536, 8960, 151936, 12, 2, 128, true>};
+  const int which = 2 * qwen15 + kb;
+  const void *fn = fns[which];
+  static bool attr_set[4] = {false, false, false, false};
+  if (!attr_set[which]) {
     hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxLds);
     if (e != hipSuccess) return e;
-    attr_set[qwen15] = true;
+    attr_set[which] = true;
   }
   void *params[] = {&args};
   return hipLaunchCooperativeKernel(fn, dim3(NB), dim3(NT), params, (unsigned)smem, s);

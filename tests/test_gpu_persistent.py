@@ -115,6 +115,48 @@ def test_persistent_small_models(tmp_path, dims):
     k.close()
 
 
+@pytest.mark.parametrize("dims", SMALL[:2] + SMALL[3:])
+def test_persistent_bf16_cache(tmp_path, dims, persist_kernel):
+    """A bf16 KV cache: the first cooperative kernel stores and reads bf16
+    rows (rounded to nearest even, as the per-kernel path stores them). Both
+    paths against the f32-cache oracle: the cache rounding moves logits by up
+    to ~1e-2 relative, so ids must agree wherever the oracle's top-2 gap is
+    above 5e-2, and the two paths must agree with each other as closely."""
+    if persist_kernel == "stream":
+        pytest.skip("the streamed kernel reads an f32 cache: a bf16 cache takes the per-kernel path")
+    s = shape_dict(*dims, 1e-6)
+    t = random_map(s, seed=sum(dims) + 3, std=0.05)
+    path = str(tmp_path / "m.safetensors")
+    write_safetensors(path, t)
+    g = myos.Model.open(path, to_block_shape(s), myos.KV_BF16, 80)
+    if g.decode_path() != myos.DECODE_PERSISTENT:
+        g.close()
+        pytest.skip("the device cannot hold the cooperative decode grid")
+    k = myos.Model.open(path, to_block_shape(s), myos.KV_BF16, 80)
+    k.set_decode_mode(myos.DECODE_KERNELS)
+    o = oracle.Model(s, t, 80, threads=4)
+    prompt = np.random.default_rng(13).integers(0, s["vocab"], 17)
+    for m in (g, k):
+        m.prefill(prompt)
+    assert o.prefill(prompt) == 0
+    ids_g, ids_k = g.greedy_decode(30), k.greedy_decode(30)
+    ids_o, gaps = oracle_steps(o, 30)
+    for i in range(30):
+        if ids_g[i] != ids_o[i] or ids_k[i] != ids_o[i]:
+            assert gaps[i] <= 5e-2, f"id {i}: {ids_g[i]} / {ids_k[i]} != {ids_o[i]} at gap {gaps[i]:.3e}"
+            break
+    if ids_g == ids_k:
+        assert max_rel(g.logits(), k.logits()) < 2e-2
+        for layer in range(s["num_layers"]):
+            for pos in (0, 16, 17, 40):
+                kg, vg = g.kv(layer, 0, pos)
+                kk, vk = k.kv(layer, 0, pos)
+                assert max_rel(kg, kk) < 2e-2 and max_rel(vg, vk) < 2e-2, (layer, pos)
+    assert g.cache_len() == k.cache_len() == 47
+    g.close()
+    k.close()
+
+
 def test_persistent_until_cache_full(tmp_path):
     s = shape_dict(256, 4, 2, 64, 512, 1000, 2, 1e-6)
     t = random_map(s, seed=5, std=0.05)
