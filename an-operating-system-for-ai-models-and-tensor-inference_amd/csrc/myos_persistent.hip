@@ -577,8 +577,8 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
   // so loads go out right after a wait returns and drain while the next
   // phase computes, each batch as soon as its registers are free:
   //   after the items of l (before the merge): o(l), gate/up slots 1-4 of l
-  //   after the attention wait of l:           QKV(l+1)
   //   during gate/up(l), after slot 0's dots:  gate/up slot 0 of l+1
+  //   after the h wait of l:                   QKV(l+1)
   // A wave that issues more loads than its memory queue holds stalls at the
   // issue, so big batches go out where the wave would wait anyway. Loads into
   // LDS make the compiler wait for them before the wave's next LDS access,
@@ -923,7 +923,6 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
       // ---- o projection + residual (tag T + P_XO) -----------------------------
       tgather_lin<3>(a.tatt, qdim, T + P_ATT, att, a, &fail_s);
       mark(a, s, 3 + 5 * l);
-      if (l + 1 < a.L) issue_q(l + 1, true);
       if (has_x) {
         const float y = dotrow<HC>(wo, att, qdim, lane);
         if (lane == 0) {
@@ -969,6 +968,7 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
           },
           a, &fail_s);
       mark(a, s, 5 + 5 * l);
+      if (l + 1 < a.L) issue_q(l + 1, true);
 
       if (has_x) {
         const float y = dotrow_lds_p(wd_s, hh, hl, I, lane);
