@@ -576,9 +576,9 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
   // vector loads, which queue behind every load the CU issued before them,
   // so loads go out right after a wait returns and drain while the next
   // phase computes, each batch as soon as its registers are free:
-  //   after the items of l (before the merge): o(l), gate/up slots 1-4 of l
+  //   after the items of l (before the merge): gate/up slots 1-4 of l
   //   during gate/up(l), after slot 0's dots:  gate/up slot 0 of l+1
-  //   after the h wait of l:                   QKV(l+1)
+  //   after the h wait of l:                   QKV(l+1), o(l+1)
   // A wave that issues more loads than its memory queue holds stalls at the
   // issue, so big batches go out where the wave would wait anyway. Loads into
   // LDS make the compiler wait for them before the wave's next LDS access,
@@ -611,6 +611,7 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
   // what layer l needs loaded before its first wait
   auto issue_first = [&](int l) {
     issue_q(l, true);
+    issue_o(l, true);
     issue_gu(l, true, 0);
     issue_down(l, true, 0);
     issue_down(l, true, 1);
@@ -882,7 +883,6 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
         __syncthreads();
       }
 
-      issue_o(l, true);
       issue_gu(l, true, 1);
       issue_gu(l, true, 2);
       issue_gu(l, true, 3);
@@ -968,7 +968,10 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
           },
           a, &fail_s);
       mark(a, s, 5 + 5 * l);
-      if (l + 1 < a.L) issue_q(l + 1, true);
+      if (l + 1 < a.L) {
+        issue_q(l + 1, true);
+        issue_o(l + 1, true);
+      }
 
       if (has_x) {
         const float y = dotrow_lds_p(wd_s, hh, hl, I, lane);
