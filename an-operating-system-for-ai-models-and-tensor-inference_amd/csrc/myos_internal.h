@@ -142,6 +142,8 @@ struct PersistLayer {
   const uint16_t *ln1, *wqkv, *wo, *ln2, *wgu, *wd;
   const float *bqkv;
   const uint16_t *wdT;         // down transposed [I][H] (streamed kernel only)
+  // down as column pairs [I/2][H]: word (j, r) = (wd[r][2j], wd[r][2j+1]) (first kernel)
+  const uint32_t *wdp;
 };
 struct PersistArgs {
   int H, I, V, L, nq, nkv, d, max_seq, qkv_rows;
@@ -154,6 +156,7 @@ struct PersistArgs {
   // tagged exchange buffers (zeroed once; tags only grow)
   uint64_t *tq, *tkv, *tpart, *tatt, *txo, *th, *txd, *targ;
   uint64_t *tpd;               // streamed kernel: [grid][H] down partials per workgroup
+  uint64_t *tpr;               // first kernel: down partials, [owner][grid][rows per owner]
   int ring_slots;              // streamed kernel: set by the launcher
   // outputs
   float *logits, *normed, *x_out;
@@ -186,6 +189,9 @@ bool stream_device_ok(const PersistArgs &a);
 hipError_t launch_decode_stream(const PersistArgs &a, hipStream_t s);
 size_t stream_tpd_words(int H);  // words of the down-partial buffer
 size_t stream_part_words(int nq, int max_seq, int d);  // attention partial words
+// dst[c][r] = src[r][c] for a [rows, cols] matrix of 32-bit words
+hipError_t launch_transpose_u32(uint32_t *dst, const uint32_t *src, int rows, int cols,
+                                hipStream_t s);
 hipError_t launch_transpose_bf16(uint16_t *dst, const uint16_t *src, int rows, int cols,
                                  hipStream_t s);
 

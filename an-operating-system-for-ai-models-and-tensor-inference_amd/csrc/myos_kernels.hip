@@ -1012,6 +1012,21 @@ __global__ void transpose_bf16_kernel(uint16_t *dst, const uint16_t *src, int ro
   }
 }
 
+__global__ void transpose_u32_kernel(uint32_t *dst, const uint32_t *src, int rows, int cols) {
+  __shared__ uint32_t t[32][33];
+  const int c0 = blockIdx.x * 32, r0 = blockIdx.y * 32;
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;  // 256 threads: 8 rows a pass
+  for (int y = ty; y < 32; y += 8) {
+    const int r = r0 + y, c = c0 + tx;
+    if (r < rows && c < cols) t[y][tx] = src[(size_t)r * cols + c];
+  }
+  __syncthreads();
+  for (int y = ty; y < 32; y += 8) {
+    const int c = c0 + y, r = r0 + tx;
+    if (r < rows && c < cols) dst[(size_t)c * rows + r] = t[tx][y];
+  }
+}
+
 // Causal prefill attention for head_dim D in {32, 64, 128}: workgroup = (query
 // head, 16 queries), 8 lanes per query each own D / 8 adjacent dims; keys and
 // values stream through LDS in tiles of 32. Per tile all 32 scores are formed
@@ -1365,6 +1380,14 @@ hipError_t launch_transpose_bf16(uint16_t *dst, const uint16_t *src, int rows, i
                                  hipStream_t s) {
   if (rows <= 0 || cols <= 0) return hipSuccess;
   hipLaunchKernelGGL(transpose_bf16_kernel, dim3(nblk(cols, 32), nblk(rows, 32)), dim3(256), 0, s,
+                     dst, src, rows, cols);
+  return hipGetLastError();
+}
+
+hipError_t launch_transpose_u32(uint32_t *dst, const uint32_t *src, int rows, int cols,
+                                hipStream_t s) {
+  if (rows <= 0 || cols <= 0) return hipSuccess;
+  hipLaunchKernelGGL(transpose_u32_kernel, dim3(nblk(cols, 32), nblk(rows, 32)), dim3(256), 0, s,
                      dst, src, rows, cols);
   return hipGetLastError();
 }

@@ -97,7 +97,8 @@ struct myos_model {
   PersistLayer *dlayers = nullptr;
   PersistArgs pargs{};            // all but tag_base / steps / pos0
   bool persist_stream = false;    // the streamed kernel (myos_stream.hip) runs it
-  uint16_t *wdT = nullptr;        // streamed kernel: down transposed, [L][I][H]
+  uint16_t *wdT = nullptr;        // streamed kernel: down transposed, [L][I][H];
+                                  // first kernel: down as column pairs, [L][I/2][H] words
   uint32_t tag_base = 1;          // tags below this value are spent
   uint32_t *err = nullptr;
   uint64_t *trace = nullptr;      // phase timestamps (myos_set_decode_trace)
@@ -431,23 +432,28 @@ int setup_persistent(myos_model *m) {
   const bool want_stream = pk && std::string(pk) == "stream";
   if (m->kv_bf16 && want_stream) return MYOS_OK;  // per-kernel path
   a.tpd = nullptr;
+  a.tpr = nullptr;
   m->persist_stream = want_stream && stream_device_ok(a);
   if (!m->persist_stream && !persist_device_ok(a)) return MYOS_OK;
-  const size_t words[9] = {m->q_dim, 2 * m->kv_dim,
-                           std::max(persist_part_words(a.nq, a.max_seq, a.d),
-                                    stream_part_words(a.nq, a.max_seq, a.d)),
-                           m->q_dim, s.hidden,
-                           s.intermediate, s.hidden, 2 * (size_t)persist_grid(),
-                           m->persist_stream ? stream_tpd_words((int)s.hidden) : 0};
+  const size_t words[10] = {m->q_dim, 2 * m->kv_dim,
+                            std::max(persist_part_words(a.nq, a.max_seq, a.d),
+                                     stream_part_words(a.nq, a.max_seq, a.d)),
+                            m->q_dim, s.hidden,
+                            s.intermediate, s.hidden, 2 * (size_t)persist_grid(),
+                            m->persist_stream ? stream_tpd_words((int)s.hidden) : 0,
+                            m->persist_stream ? 0
+                                              : (size_t)persist_grid() * persist_grid() *
+                                                    ((s.hidden + persist_grid() - 1) / persist_grid())};
   size_t total = 0;
   for (size_t w : words) total += align256(w * 8);
   total += 256;  // error word
   HIP_TRY(hipMalloc((void **)&m->pbuf, total));
   HIP_TRY(hipMemsetAsync(m->pbuf, 0, total, m->stream));
   m->pbuf_bytes = total;
-  uint64_t **dst[9] = {&a.tq, &a.tkv, &a.tpart, &a.tatt, &a.txo, &a.th, &a.txd, &a.targ, &a.tpd};
+  uint64_t **dst[10] = {&a.tq,  &a.tkv, &a.tpart, &a.tatt, &a.txo,
+                        &a.th,  &a.txd, &a.targ,  &a.tpd,  &a.tpr};
   uint8_t *p = m->pbuf;
-  for (int i = 0; i < 9; i++) {
+  for (int i = 0; i < 10; i++) {
     *dst[i] = (uint64_t *)p;
     p += align256(words[i] * 8);
   }
@@ -455,17 +461,24 @@ int setup_persistent(myos_model *m) {
   a.err = m->err;
   std::vector<PersistLayer> hl(s.num_layers);
   const size_t dsz = s.intermediate * s.hidden;  // elements of one down matrix
-  if (m->persist_stream) {
-    // the streamed kernel reads down by columns: keep a transposed copy
-    HIP_TRY(hipMalloc((void **)&m->wdT, s.num_layers * dsz * 2));
-    for (size_t l = 0; l < s.num_layers; l++)
+  // both cooperative kernels read down by columns: the streamed one as a
+  // transposed copy, the first one as column pairs (one word per row of a pair)
+  HIP_TRY(hipMalloc((void **)&m->wdT, s.num_layers * dsz * 2));
+  for (size_t l = 0; l < s.num_layers; l++) {
+    if (m->persist_stream)
       HIP_TRY(launch_transpose_bf16(m->wdT + l * dsz, m->layers[l].wd, (int)s.hidden,
                                     (int)s.intermediate, m->stream));
+    else
+      HIP_TRY(launch_transpose_u32((uint32_t *)(m->wdT + l * dsz),
+                                   (const uint32_t *)m->layers[l].wd, (int)s.hidden,
+                                   (int)s.intermediate / 2, m->stream));
   }
   for (size_t l = 0; l < s.num_layers; l++) {
     const DevLayer &L = m->layers[l];
+    uint16_t *t = m->wdT + l * dsz;
     hl[l] = PersistLayer{L.ln1, L.wqkv, L.wo, L.ln2, L.wgu, L.wd, L.bqkv,
-                         m->wdT ? m->wdT + l * dsz : nullptr};
+                         m->persist_stream ? t : nullptr,
+                         m->persist_stream ? nullptr : (const uint32_t *)t};
   }
   HIP_TRY(hipMalloc((void **)&m->dlayers, hl.size() * sizeof(PersistLayer)));
   HIP_TRY(hipMemcpy(m->dlayers, hl.data(), hl.size() * sizeof(PersistLayer),

@@ -1,10 +1,11 @@
 // Persistent greedy-decode kernel for MI355X (gfx950).
 //
 // One cooperative launch of 256 workgroups (one per CU, 512 threads) runs a
-// whole run of decode steps. Every workgroup owns fixed rows of every
-// projection (QKV, o, gate/up, down, head) and a fixed slice of the residual
-// stream; attention work items (kv head, 32-position chunk) are dealt round
-// robin. Activations cross workgroups as 64-bit words (value, tag), stored and
+// whole run of decode steps. Every workgroup owns fixed rows of the QKV, o,
+// gate/up and head projections and a fixed slice of the residual stream; a
+// gate/up owner also owns the down columns of its h values, so down runs as
+// per-workgroup partial sums that the residual-row owners add up. Attention
+// work items (kv head, 32-position chunk) are dealt round robin. Activations cross workgroups as 64-bit words (value, tag), stored and
 // loaded with device-coherent (sc1) accesses; the tag names the step, layer
 // and phase that produced the value. A consumer re-polls exactly the words it
 // needs until they carry the expected tag, so the only synchronisation is the
@@ -30,7 +31,7 @@ constexpr int NT = 512;              // threads per workgroup
 constexpr int NW = NT / 64;          // wavefronts per workgroup
 constexpr int NB = 256;              // workgroups (one per CU)
 constexpr int HC = 3;                // 8-column chunks per lane, k <= 1536
-constexpr int MAXI = 9216;           // intermediate limit (down rows staged in LDS)
+constexpr int MAXI = 9216;           // intermediate limit
 constexpr int GPMAX = 5;             // gate/up row pairs per wavefront
 constexpr int AC = 32;               // attention positions per work item
 constexpr int HT = 2;                // head rows per tile
@@ -42,7 +43,7 @@ constexpr unsigned kSpinMax = 1u << 20;
 // A word's tag is its step's base + kTPL * layer + phase; the head's partials
 // take base + kTPL * layers; a step spans kTPL * layers + 2 tags.
 constexpr uint32_t kTPL = 6;
-constexpr uint32_t P_QKV = 0, P_PART = 1, P_XO = 2, P_H = 3, P_XD = 4, P_ATT = 5;
+constexpr uint32_t P_QKV = 0, P_PART = 1, P_XO = 2, P_PD = 3, P_XD = 4, P_ATT = 5;
 constexpr size_t kMaxLds = 159 * 1024;  // dynamic LDS: 160 KB per workgroup on gfx950 less the static part
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -257,26 +258,27 @@ __device__ __forceinline__ void ldrow_all(u32x4 (&t)[C], const uint16_t *W, int 
   }
 }
 
-// Part `part` of `nparts` of one row streamed into LDS with direct (DMA)
-// loads: chunk c of the row lands at dst + 16 c, and this part covers the
-// 1 KB wave loads [part * per, (part + 1) * per), so a row's bytes can be
-// spread over several waits. `dst` must be wave-uniform; no registers hold
-// the row meanwhile. The compiler waits for these loads before the wave's
-// next LDS access.
-__device__ __forceinline__ void dma_row_part(const uint16_t *W, int k, int row, uint8_t *dst,
-                                             int lane, int part, int nparts) {
-  const int nch = k >> 3;
-  const int nld = (nch + 63) >> 6, per = (nld + nparts - 1) / nparts;
+// Part `part` of 3 of a block of the column-pair matrix P (rows of `ld`
+// words) streamed into LDS with direct (DMA) loads: rows [j0, j0 + kv),
+// columns [c0, c0 + cw) land row-major at dst (word q = row * cw + col), 1 KB
+// per wave load, and part p covers loads [p per, (p + 1) per), so a block can
+// be spread over several waits. cw % 4 == 0; `dst` is wave-uniform; no
+// registers hold the block meanwhile. The compiler waits for these loads
+// before the wave's next LDS access.
+__device__ __forceinline__ void dma_block(const uint32_t *P, int ld, int j0, int kv, int c0, int cw,
+                                          uint8_t *dst, int lane, int part) {
+  const int tot = kv * cw, nld = (tot + 255) >> 8, per = (nld + 2) / 3;
   const int i0 = part * per, i1 = min(i0 + per, nld);
-  const __amdgpu_buffer_rsrc_t rs = wrsrc(W);
-  // the 1 KB step rides in the scalar offset: one lane offset serves every load
-  const int soff = row * k * 2;
+  const __amdgpu_buffer_rsrc_t rs = wrsrc((const uint16_t *)P);
+  const int soff = (j0 * ld + c0) * 4;
   for (int i = i0; i < i1; i++) {
-    const int c = lane + i * 64;
-    if (c < nch)
+    const int q = i * 256 + lane * 4;
+    if (q < tot) {
+      const int row = q / cw, col = q - row * cw;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          rs, (__attribute__((address_space(3))) void *)(dst + i * 1024), 16, lane * 16,
-          soff + i * 1024, 0, 2 /* nt */);
+          rs, (__attribute__((address_space(3))) void *)(dst + i * 1024), 16,
+          (row * ld + col) * 4, soff, 0, 2 /* nt */);
+    }
   }
 }
 
@@ -448,28 +450,6 @@ __device__ __forceinline__ float dotrow_p(const u32x4 (&t)[C], const XPairs<C> &
   return wave_sum(s);
 }
 
-// A row held in LDS (16 bytes per 8-column chunk) times x held in LDS as bf16
-// hi and lo planes (x = hi + lo, see XPairs)
-__device__ __forceinline__ float dotrow_lds_p(const uint8_t *wl, const uint16_t *xh,
-                                              const uint16_t *xl, int k, int lane) {
-  const int nch = k >> 3;
-  float s = 0.f;
-#pragma unroll 4
-  for (int c = lane; c < nch; c += 64) {
-    const u32x4 w = *(const u32x4 *)(wl + c * 16);
-    const u32x4 h = *(const u32x4 *)(xh + c * 8), l = *(const u32x4 *)(xl + c * 8);
-    s = dot2(w.x, h.x, s);
-    s = dot2(w.x, l.x, s);
-    s = dot2(w.y, h.y, s);
-    s = dot2(w.y, l.y, s);
-    s = dot2(w.z, h.z, s);
-    s = dot2(w.z, l.z, s);
-    s = dot2(w.w, h.w, s);
-    s = dot2(w.w, l.w, s);
-  }
-  return wave_sum(s);
-}
-
 __device__ __forceinline__ float silu(float z) { return z / (1.0f + expf(-z)); }
 
 // A pointer read from LDS, made provably wave-uniform: kept in scalar
@@ -491,7 +471,7 @@ __device__ __forceinline__ int opaque(int v) {
 
 // phase timestamps of one step (100 MHz device clock), thread 0 of each
 // workgroup: slot 0 token chosen; 1 + 5 l + {0 x ready, 1 attention items
-// done, 2 attention merged, 3 X_o ready, 4 h ready}; 1 + 5 L head input ready;
+// done, 2 attention merged, 3 X_o ready, 4 down partials ready}; 1 + 5 L head input ready;
 // 2 + 5 L head done
 __device__ __forceinline__ void mark(const PersistArgs &a, uint32_t s, int slot) {
   if (a.trace && s == a.trace_step && threadIdx.x == 0)
@@ -509,6 +489,26 @@ __device__ __forceinline__ void kvstore(uint8_t *base, size_t idx, float v) {
     cstore((float *)base + idx, v);
 }
 
+// Gate/up ownership: h values [np * (wg - gst), np * (wg - gst + 1)) go to
+// workgroup wg in [gst, gen), np even so a workgroup's share is whole column
+// pairs of down. The workgroups that run no attention item (the first
+// nkv * nchmax) and no merge (the last nq) take them when they can hold
+// them: the attention chain's workgroups then carry almost no weight loads
+// into their waits. Otherwise every workgroup takes a share. Returns np.
+__host__ __device__ inline int gu_share(int I, int nkv, int nchmax, int nq, int *gst, int *gen) {
+  const int cap = GPMAX * NW;
+  int a = nkv * nchmax, b = NB - nq;
+  int np = b - a > 0 ? 2 * ((I + 2 * (b - a) - 1) / (2 * (b - a))) : cap + 1;
+  if (np > cap) {
+    a = 0;
+    b = NB;
+    np = 2 * ((I + 2 * NB - 1) / (2 * NB));
+  }
+  *gst = a;
+  *gen = b;
+  return np;
+}
+
 // Every dimension of the model is a template constant, or 0 to read it from
 // the launch arguments: the launcher picks the Qwen2.5-1.5B instantiation for
 // that shape, where folding the dimensions frees the scalar registers that
@@ -519,8 +519,8 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
   extern __shared__ float4 sm4[];
   float *xs = (float *)sm4;     // [MAXH] activation for the current phase
   float *att = xs + MAXH;       // [MAXH] attention output
-  float *big = att + MAXH;      // phase scratch: h [I] / attention staging / merge weights
-  uint8_t *wdl = (uint8_t *)(xs + a.lds_wd);  // [rows per workgroup][I] bf16 down rows
+  float *big = att + MAXH;      // phase scratch: attention staging / merge / h share
+  uint8_t *wdl = (uint8_t *)(xs + a.lds_wd);  // [NW][kp][cw] down column pairs
   __shared__ float xl[NW];      // this workgroup's rows of the residual stream
   __shared__ int fail_s;
   __shared__ uint32_t tok_s;
@@ -543,18 +543,17 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
   const int q0 = wg * qper, q1 = min(q0 + qper, qkv_rows);
   const int xper = (H + NB - 1) / NB;
   const int x0 = wg * xper, x1 = min(x0 + xper, H);
-  // Gate/up pairs go to the workgroups that run no attention item (the
-  // first nkv * nchmax) and no merge (the last nq) when those can hold them:
-  // the attention chain's workgroups then carry almost no weight loads into
-  // their waits. Otherwise every workgroup takes a share.
-  int gst = nkv * nchmax, gen = NB - nq;
-  if (gen - gst <= 0 || (gen - gst) * GPMAX * NW < I) {
-    gst = 0;
-    gen = NB;
-  }
-  const int gper = 2 * ((I + (gen - gst) - 1) / (gen - gst));
+  int gst, gen;
+  const int np = gu_share(I, nkv, nchmax, nq, &gst, &gen);
+  const int gper = 2 * np;  // gate/up rows
   const int g0 = wg >= gst && wg < gen ? (wg - gst) * gper : 2 * I;
   const int g1 = min(g0 + gper, 2 * I);
+  const int nact = (I + np - 1) / np;  // workgroups gst .. gst + nact - 1 hold h values
+  // down as column pairs: this workgroup's h values pair up into kv rows of
+  // P = [I / 2][H], from row j0; wave w takes columns [w cw, (w + 1) cw)
+  const int kp = np >> 1, j0 = g0 >> 2;
+  const int kv = max(0, min(kp, (I >> 1) - j0));
+  const int cw = H / NW;
   const int vper = (V + NB - 1) / NB;
   const int v0 = wg * vper, v1 = min(v0 + vper, V);
   const int qrow = q0 + 2 * wave;      // this wave's QKV pair
@@ -564,7 +563,7 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
   // The layer table, copied to LDS once: a weight pointer read from global
   // memory inside the loop would be a vector load whose wait (vmcnt 0) also
   // waits for every weight load in flight.
-  PersistLayer *lay = (PersistLayer *)(wdl + (size_t)xper * I * 2);
+  PersistLayer *lay = (PersistLayer *)(wdl + (size_t)NW * kp * cw * 4);
   for (int i = tid; i < a.L * (int)(sizeof(PersistLayer) / 8); i += NT)
     ((uint64_t *)lay)[i] = ((const uint64_t *)a.layers)[i];
   if (tid == 0) fail_s = 0;
@@ -572,23 +571,25 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
   __syncthreads();
 
   // Weight rows held on chip across phases: this wave's QKV pair, o row and
-  // gate/up pairs in registers, its down row in LDS. A wait re-polls with
-  // vector loads, which queue behind every load the CU issued before them,
-  // so loads go out right after a wait returns and drain while the next
-  // phase computes, each batch as soon as its registers are free:
+  // gate/up pairs in registers, its block of down column pairs in LDS. A
+  // wait re-polls with vector loads, which queue behind every load the CU
+  // issued before them, so loads go out right after a wait returns and drain
+  // while the next phase computes, each batch as soon as its registers are
+  // free:
   //   after the items of l (before the merge): gate/up slots 1-4 of l
   //   during gate/up(l), after slot 0's dots:  gate/up slot 0 of l+1
-  //   after the h wait of l:                   QKV(l+1), o(l+1)
+  //   after the down partials of l:            QKV(l+1), o(l+1)
   // A wave that issues more loads than its memory queue holds stalls at the
   // issue, so big batches go out where the wave would wait anyway. Loads into
   // LDS make the compiler wait for them before the wave's next LDS access,
-  // so the down row goes just before a wait:
-  //   after o(l): part 2 of l;   after down(l): parts 0, 1 of l+1
+  // so the down block goes in three parts, each just before a wait: before
+  // the x wait of l, after QKV(l) and after o(l). (One batch after QKV(l)
+  // is 9 % slower: the attention-output wait then drains all of it.)
   // Layer 0's first share loads after the head, so that no weight row is
   // live across the head's own tiles.
   u32x4 wq0[HC], wq1[HC], wo[HC];
   u32x4 gu[GPMAX][2][HC];  // gate/up slot p: rows (2i, 2i+1) = (gate_i, up_i)
-  uint8_t *wd_s = wdl + (size_t)wave * I * 2;  // this wave's down row
+  uint8_t *wp_s = wdl + (size_t)wave * kp * cw * 4;  // this wave's down block
 
   // gate/up pair in slot p of this wavefront
   auto gu_row = [&](int p) { return g0 + 2 * (wave + p * NW); };
@@ -605,16 +606,15 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
     ldrow<HC>(gu[p][0], w, H, row, ok, lane);
     ldrow<HC>(gu[p][1], w, H, row + 1, ok, lane);
   };
-  auto issue_down = [&](int l, bool v, int part) {
-    if (v && has_x) dma_row_part(uni(lay[l].wd), I, xrow, wd_s, lane, part, 3);
+  auto issue_wdp = [&](int l, int part) {
+    if (kv > 0) dma_block(uni(lay[l].wdp), H, j0, kv, wave * cw, cw, wp_s, lane, part);
   };
   // what layer l needs loaded before its first wait
   auto issue_first = [&](int l) {
+    issue_wdp(l, 0);
     issue_q(l, true);
     issue_o(l, true);
     issue_gu(l, true, 0);
-    issue_down(l, true, 0);
-    issue_down(l, true, 1);
   };
 
   issue_first(0);
@@ -735,6 +735,8 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
           // gather's loads (vmcnt 0) also waits for these stores.
         }
       }
+
+      issue_wdp(l, 1);
 
       // ---- attention partials for (kv head, chunk) items (tag T + P_PART) ----
       // Thread i = tid + u NT holds columns [4 j4, 4 j4 + 4) of position
@@ -930,9 +932,9 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
           tput(a.txo + xrow, xl[wave], T + P_XO);
         }
       }
-      issue_down(l, true, 2);
 
-      // ---- gate/up + SwiGLU (tag T + P_H) -------------------------------------
+      issue_wdp(l, 2);
+      // ---- gate/up + SwiGLU + down partials (tag T + P_PD) ----------------------
       load_gw<HC>(gw, Lln2, H, lane);
       tgather_lin<3>(a.txo, H, T + P_XO, xs, a, &fail_s);
       mark(a, s, 4 + 5 * l);
@@ -949,40 +951,69 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
           if (p == 0 && l + 1 < a.L) issue_gu(l + 1, true, 0);
         }
       }
+      // this workgroup's h values, local index wave + p NW, land in LDS
+      float *hs = big;
 #pragma unroll
-      for (int p = 0; p < GPMAX; p++) {
-        const int row = gu_row(p);
-        if (row < g1 && lane == 0) tput(a.th + (row >> 1), silu(gy[p][0]) * gy[p][1], T + P_H);
-      }
-
-
-      // ---- down + residual (tag T + P_XD) -------------------------------------
-      // h lands in LDS as bf16 hi and lo planes for the down row's dot2
-      uint16_t *hh = (uint16_t *)big, *hl = hh + I;
-      tgather_lin_to<18>(
-          a.th, I, T + P_H,
-          [hh, hl](int i, float v) {
-            const uint32_t p = pack_bf16(v, 0.f);
-            hh[i] = (uint16_t)p;
-            hl[i] = (uint16_t)pack_bf16(v - bf_lo(p), 0.f);
-          },
-          a, &fail_s);
-      mark(a, s, 5 + 5 * l);
-      if (l + 1 < a.L) {
-        issue_q(l + 1, true);
-        issue_o(l + 1, true);
-      }
-
-      if (has_x) {
-        const float y = dotrow_lds_p(wd_s, hh, hl, I, lane);
-        if (lane == 0) {
-          xl[wave] += y;
-          tput(a.txd + xrow, xl[wave], T + P_XD);
+      for (int p = 0; p < GPMAX; p++)
+        if (gu_row(p) < g1 && lane == 0) hs[wave + p * NW] = silu(gy[p][0]) * gy[p][1];
+      __syncthreads();
+      // down partials: column r of the wave's block times the workgroup's h,
+      // h split into bf16 hi + lo pairs (see XPairs), one word per row pair
+      if (kv > 0) {
+        constexpr int CWC = (MAXH / NW + 63) / 64;
+        float acc[CWC];
+#pragma unroll
+        for (int i = 0; i < CWC; i++) acc[i] = 0.f;
+        const uint32_t *wp = (const uint32_t *)wp_s;
+        for (int j = 0; j < kv; j++) {
+          const float2 h2 = *(const float2 *)(hs + 2 * j);
+          const uint32_t hp = pack_bf16(h2.x, h2.y);
+          const uint32_t lp = pack_bf16(h2.x - bf_lo(hp), h2.y - bf_hi(hp));
+#pragma unroll
+          for (int i = 0; i < CWC; i++) {
+            const int c = lane + i * 64;
+            if (c < cw) {
+              const uint32_t w = wp[j * cw + c];
+              acc[i] = dot2(w, lp, dot2(w, hp, acc[i]));
+            }
+          }
+        }
+        // row r goes to its owner b = r / xper: tpr[b][wg][r - b xper], the
+        // block of b holding nx_b = min(xper, H - b xper) words per workgroup
+#pragma unroll
+        for (int i = 0; i < CWC; i++) {
+          const int c = lane + i * 64;
+          if (c < cw) {
+            const int r = wave * cw + c, b = r / xper, nxb = min(xper, H - b * xper);
+            tput(a.tpr + (size_t)b * NB * xper + wg * nxb + (r - b * xper), acc[i], T + P_PD);
+          }
         }
       }
+
+      // ---- down + residual (tag T + P_XD) -------------------------------------
+      // this workgroup's block: nact partials of each of its nx rows, in one
+      // contiguous gather; wave w sums row x0 + w in a fixed order
+      {
+        const int nx = x1 - x0;
+        float *pr = big + 64;  // past the h share, which other waves may still read
+        if (nx > 0)
+          tgather_lin<3>(a.tpr + (size_t)wg * NB * xper + (size_t)gst * nx, nact * nx, T + P_PD, pr, a,
+                         &fail_s);
+        if (has_x) {
+          float sum = 0.f;
+          for (int k = lane; k < nact; k += 64) sum += pr[k * nx + wave];
+          const float y = wave_sum(sum);
+          if (lane == 0) {
+            xl[wave] += y;
+            tput(a.txd + xrow, xl[wave], T + P_XD);
+          }
+        }
+      }
+      mark(a, s, 5 + 5 * l);
       if (l + 1 < a.L) {
-        issue_down(l + 1, true, 0);
-        issue_down(l + 1, true, 1);
+        issue_wdp(l + 1, 0);
+        issue_q(l + 1, true);
+        issue_o(l + 1, true);
       }
 
     }
@@ -1109,35 +1140,42 @@ size_t persist_part_words(int nq, int max_seq, int d) {
 }
 
 bool persist_supported(int H, int I, int qdim, int d, int gq) {
-  if (H % 8 || I % 8 || qdim % 8) return false;
+  // H % 32: each wave's H / 8 down columns load 4 words a lane
+  if (H % 32 || I % 8 || qdim % 8) return false;
   if (H > MAXH || qdim > MAXH || I > MAXI) return false;
   // the attention items sum a score over d / 4 lanes: d in {32, 64, 128}
   if ((d & (d - 1)) || d < 32 || d > MAXD || gq > 8) return false;
   // each workgroup's gate/up pairs fit GPMAX per wavefront, residual rows and
   // QKV pairs one per wavefront
-  const int gper = (((2 * I + NB - 1) / NB) + 1) & ~1;
-  if (gper / 2 > GPMAX * NW) return false;
+  if (2 * ((I + 2 * NB - 1) / (2 * NB)) > GPMAX * NW) return false;
   if ((H + NB - 1) / NB > NW) return false;
   const int qkv_rows = qdim + 2 * (qdim / gq);
   if ((((qkv_rows + NB - 1) / NB) + 1) / 2 > NW) return false;
   return true;
 }
 
-// LDS bytes one workgroup needs: activations, the largest phase scratch, and
-// this workgroup's down rows; sets the down-row offset in `a`
+// LDS bytes one workgroup needs: activations, the largest phase scratch
+// (attention item staging, merge partials, argmax partials, h share), this
+// workgroup's down column pairs and the layer table; sets the down block's
+// offset in `a`
 static size_t persist_lds(PersistArgs &a) {
   const int gq = a.nq / a.nkv;
-  const size_t attn = (size_t)gq * a.d + AC * (a.d + 1) + AC * a.d + gq * AC + 2 * gq + 2 * a.d;
-  const size_t nchm = (size_t)(a.max_seq + AC - 1) / AC;
-  const size_t merge = nchm * (a.d + 2) + nchm;
-  size_t big = (size_t)a.I;
-  if (attn > big) big = attn;
+  const size_t attn = (size_t)gq * a.d + a.d + (size_t)AC * a.d + (size_t)gq * AC;
+  const int nchm = (a.max_seq + AC - 1) / AC;
+  const size_t merge = (size_t)nchm * (a.d + 2) + nchm;
+  int gst, gen;
+  const int np = gu_share(a.I, a.nkv, nchm, a.nq, &gst, &gen);
+  size_t big = attn;
   if (merge > big) big = merge;
   if ((size_t)2 * NB > big) big = 2 * NB;
-  const size_t wd_off = 2 * MAXH + ((big + 3) & ~(size_t)3);  // floats
+  if ((size_t)np > big) big = np;
   const size_t xper = (size_t)(a.H + NB - 1) / NB;
+  if (64 + NB * xper > big) big = 64 + NB * xper;  // h share, then the down partials
+  if (np > 64) return kMaxLds + 1;
+  const size_t wd_off = 2 * MAXH + ((big + 3) & ~(size_t)3);  // floats
   a.lds_wd = (int)wd_off;
-  return wd_off * sizeof(float) + xper * (size_t)a.I * 2 + (size_t)a.L * sizeof(PersistLayer);
+  return wd_off * sizeof(float) + (size_t)NW * (np / 2) * (a.H / NW) * 4 +
+         (size_t)a.L * sizeof(PersistLayer);
 }
 
 bool persist_device_ok(const PersistArgs &a) {
