@@ -951,31 +951,54 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
           if (p == 0 && l + 1 < a.L) issue_gu(l + 1, true, 0);
         }
       }
-      // this workgroup's h values, local index wave + p NW, land in LDS
+      // this workgroup's h values, local index wave + p NW, land in LDS; lane
+      // p takes slot p, so a wave evaluates one SwiGLU instead of GPMAX in a row
       float *hs = big;
+      {
+        float g = gy[0][0], u = gy[0][1];
 #pragma unroll
-      for (int p = 0; p < GPMAX; p++)
-        if (gu_row(p) < g1 && lane == 0) hs[wave + p * NW] = silu(gy[p][0]) * gy[p][1];
+        for (int p = 1; p < GPMAX; p++)
+          if (lane == p) {
+            g = gy[p][0];
+            u = gy[p][1];
+          }
+        if (lane < GPMAX && gu_row(lane) < g1) hs[wave + lane * NW] = silu(g) * u;
+      }
       __syncthreads();
       // down partials: column r of the wave's block times the workgroup's h,
-      // h split into bf16 hi + lo pairs (see XPairs), one word per row pair
+      // h split into bf16 hi + lo pairs (see XPairs), one word per row pair.
+      // Lane j < kv packs pair j once; the unrolled loop takes pair j from
+      // lane j into scalar registers, so every LDS read of the block can be in
+      // flight at once. Rows past kv re-read row kv - 1 against a zero pair.
       if (kv > 0) {
-        constexpr int CWC = (MAXH / NW + 63) / 64;
+        constexpr int CWC = (MAXH / NW + 63) / 64, KPM = GPMAX * NW / 2;
         float acc[CWC];
 #pragma unroll
         for (int i = 0; i < CWC; i++) acc[i] = 0.f;
+        const float2 h2 = lane < kv ? *(const float2 *)(hs + 2 * lane) : make_float2(0.f, 0.f);
+        const uint32_t hpl = pack_bf16(h2.x, h2.y);
+        const uint32_t lpl = pack_bf16(h2.x - bf_lo(hpl), h2.y - bf_hi(hpl));
         const uint32_t *wp = (const uint32_t *)wp_s;
-        for (int j = 0; j < kv; j++) {
-          const float2 h2 = *(const float2 *)(hs + 2 * j);
-          const uint32_t hp = pack_bf16(h2.x, h2.y);
-          const uint32_t lp = pack_bf16(h2.x - bf_lo(hp), h2.y - bf_hi(hp));
+        const int kvm = opaque(kv - 1);  // not hoisted: per-row offsets stay unspilled
+        constexpr int RB = KPM / 2;      // rows per batch: reads first, then the dots
 #pragma unroll
-          for (int i = 0; i < CWC; i++) {
-            const int c = lane + i * 64;
-            if (c < cw) {
-              const uint32_t w = wp[j * cw + c];
-              acc[i] = dot2(w, lp, dot2(w, hp, acc[i]));
+        for (int jb = 0; jb < KPM; jb += RB) {
+          uint32_t wv[RB][CWC];
+#pragma unroll
+          for (int j = 0; j < RB; j++) {
+            const int jj = min(jb + j, kvm);
+#pragma unroll
+            for (int i = 0; i < CWC; i++) {
+              const int c = lane + i * 64;
+              wv[j][i] = c < cw ? wp[jj * cw + c] : 0u;
             }
+          }
+#pragma unroll
+          for (int j = 0; j < RB; j++) {
+            const uint32_t hp = __builtin_amdgcn_readlane(hpl, jb + j);
+            const uint32_t lp = __builtin_amdgcn_readlane(lpl, jb + j);
+#pragma unroll
+            for (int i = 0; i < CWC; i++) acc[i] = dot2(wv[j][i], lp, dot2(wv[j][i], hp, acc[i]));
           }
         }
         // row r goes to its owner b = r / xper: tpr[b][wg][r - b xper], the
