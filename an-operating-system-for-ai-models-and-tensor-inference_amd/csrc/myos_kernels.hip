@@ -1028,19 +1028,25 @@ __global__ void transpose_u32_kernel(uint32_t *dst, const uint32_t *src, int row
 }
 
 // Causal prefill attention for head_dim D in {32, 64, 128}: workgroup = (query
-// head, 16 queries), 8 lanes per query each own D / 8 adjacent dims; keys and
-// values stream through LDS in tiles of 32. Per tile all 32 scores are formed
-// first, then the running max, the rescale of the partial output and the
-// probabilities (one online-softmax step per tile). Query i sits at position
-// start + i and sees keys <= it (GqaMask::Causal, gqa.rs:80-86).
+// head, 16 queries) x KG key groups, 8 lanes per query each own D / 8 adjacent
+// dims; keys and values stream through LDS in tiles of 32. Per tile all 32
+// scores are formed first, then the running max, the rescale of the partial
+// output and the probabilities (one online-softmax step per tile). Key group
+// kg takes tiles kg, kg + KG, ... of the visible keys, each group into its own
+// LDS tile, so a short prompt's few workgroups walk 1 / KG of the tiles one
+// after another; the groups' (max, sum, output) states then merge through LDS
+// in a fixed order. Query i sits at position start + i and sees keys <= it
+// (GqaMask::Causal, gqa.rs:80-86).
 constexpr int kTq = 16, kTk = 32;
-template <int D>
-__global__ void __launch_bounds__(kTq * 8) attn_prefill_tiled_kernel(AttnPrefillArgs a) {
-  constexpr int DL = D / 8;
-  __shared__ __attribute__((aligned(16))) float k_s[kTk * D];
-  __shared__ __attribute__((aligned(16))) float v_s[kTk * D];
+template <int D, int KG>
+__global__ void __launch_bounds__(kTq * 8 * KG) attn_prefill_tiled_kernel(AttnPrefillArgs a) {
+  constexpr int DL = D / 8, NTG = kTq * 8;
+  extern __shared__ float4 attn_sm[];
+  const int tid = threadIdx.x, kg = tid / NTG, gt = tid - kg * NTG;
+  float *k_s = (float *)attn_sm + kg * 2 * kTk * D;
+  float *v_s = k_s + kTk * D;
   const int h = blockIdx.x, g = h / (a.nq / a.nkv);
-  const int tid = threadIdx.x, qi = blockIdx.y * kTq + (tid >> 3), j = tid & 7;
+  const int qi = blockIdx.y * kTq + (gt >> 3), j = gt & 7;
   const bool active = qi < a.M;
   const int qpos = a.start_pos + (active ? qi : a.M - 1);
   const int last_pos = a.start_pos + min(a.M - 1, (int)(blockIdx.y + 1) * kTq - 1);
@@ -1053,12 +1059,15 @@ __global__ void __launch_bounds__(kTq * 8) attn_prefill_tiled_kernel(AttnPrefill
     o[e] = 0.f;
   }
   float mx = -INFINITY, l = 0.f;
-  for (int t0 = 0; t0 <= last_pos; t0 += kTk) {
-    const int nt = min(kTk, last_pos + 1 - t0);
+  // every group runs the same rounds (the barriers), a group past the
+  // visible keys idles
+  for (int r0 = 0; r0 <= last_pos; r0 += KG * kTk) {
+    const int t0 = r0 + kg * kTk;
+    const int nt = max(0, min(kTk, last_pos + 1 - t0));
     __syncthreads();
     // the tile's K and V rows, 4 floats per load
     const size_t kv0 = ((size_t)g * a.max_seq + t0) * D;
-    for (int i = tid * 4; i < nt * D; i += kTq * 8 * 4) {
+    for (int i = gt * 4; i < nt * D; i += NTG * 4) {
       float4 kv, vv;
       if (a.kv_bf16) {
         const uint2 kb = *(const uint2 *)((const uint16_t *)a.kc + kv0 + i);
@@ -1073,6 +1082,7 @@ __global__ void __launch_bounds__(kTq * 8) attn_prefill_tiled_kernel(AttnPrefill
       *(float4 *)(v_s + i) = vv;
     }
     __syncthreads();
+    if (nt == 0) continue;
     float sc[kTk];
     float tmax = -INFINITY;
 #pragma unroll
@@ -1105,6 +1115,36 @@ __global__ void __launch_bounds__(kTq * 8) attn_prefill_tiled_kernel(AttnPrefill
     }
     l = l * corr + psum;
     mx = mnew;
+  }
+  if (KG > 1) {
+    // merge: group 0 combines the KG states of its query in group order
+    __syncthreads();
+    float *mo = (float *)attn_sm;                 // [KG][NTG][DL] outputs
+    float *ml = mo + KG * NTG * DL;               // [KG][NTG] (max, sum)
+    if (kg > 0) {
+#pragma unroll
+      for (int e = 0; e < DL; e++) mo[(kg * NTG + gt) * DL + e] = o[e];
+      ml[2 * (kg * NTG + gt)] = mx;
+      ml[2 * (kg * NTG + gt) + 1] = l;
+    }
+    __syncthreads();
+    if (kg > 0) return;
+    float M = mx;
+#pragma unroll
+    for (int k = 1; k < KG; k++) M = fmaxf(M, ml[2 * (k * NTG + gt)]);
+    // every query sees key 0, so M is finite
+    const float c0 = expf(mx - M);
+    l *= c0;
+#pragma unroll
+    for (int e = 0; e < DL; e++) o[e] *= c0;
+#pragma unroll
+    for (int k = 1; k < KG; k++) {
+      const float mk = ml[2 * (k * NTG + gt)];
+      const float ck = mk == -INFINITY ? 0.f : expf(mk - M);
+      l = fmaf(ml[2 * (k * NTG + gt) + 1], ck, l);
+#pragma unroll
+      for (int e = 0; e < DL; e++) o[e] = fmaf(mo[(k * NTG + gt) * DL + e], ck, o[e]);
+    }
   }
   if (!active) return;
 #pragma unroll
@@ -1356,12 +1396,36 @@ hipError_t launch_attn_prefill(const AttnPrefillArgs &a, hipStream_t s) {
   // 16-byte tile loads: the cache rows and q must be aligned to 4 elements
   if (a.head_dim == 128 || a.head_dim == 64 || a.head_dim == 32) {
     dim3 tg(a.nq, nblk((size_t)a.M, kTq));
+    // fewer workgroups than CUs: four key groups per workgroup
+    const bool split = tg.x * tg.y < 256;
+    const size_t smem = (split ? 4 : 1) * 2 * kTk * a.head_dim * sizeof(float);
+    const void *fn;
     switch (a.head_dim) {
-      case 128: hipLaunchKernelGGL(attn_prefill_tiled_kernel<128>, tg, dim3(kTq * 8), 0, s, a); break;
-      case 64: hipLaunchKernelGGL(attn_prefill_tiled_kernel<64>, tg, dim3(kTq * 8), 0, s, a); break;
-      default: hipLaunchKernelGGL(attn_prefill_tiled_kernel<32>, tg, dim3(kTq * 8), 0, s, a); break;
+      case 128:
+        fn = split ? (const void *)attn_prefill_tiled_kernel<128, 4>
+                   : (const void *)attn_prefill_tiled_kernel<128, 1>;
+        break;
+      case 64:
+        fn = split ? (const void *)attn_prefill_tiled_kernel<64, 4>
+                   : (const void *)attn_prefill_tiled_kernel<64, 1>;
+        break;
+      default:
+        fn = split ? (const void *)attn_prefill_tiled_kernel<32, 4>
+                   : (const void *)attn_prefill_tiled_kernel<32, 1>;
+        break;
     }
-    return hipGetLastError();
+    if (smem >= 64 * 1024) {  // the 4-group d = 64 and d = 128 instantiations
+      static bool attr_done[2] = {false, false};
+      bool &done = attr_done[a.head_dim == 128];
+      if (!done) {
+        hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+        if (e != hipSuccess) return e;
+        done = true;
+      }
+    }
+    AttnPrefillArgs args = a;
+    void *params[] = {&args};
+    return hipLaunchKernel(fn, tg, dim3(kTq * 8 * (split ? 4 : 1)), params, smem, s);
   }
   dim3 grid(a.nq, nblk((size_t)a.M, kPqPerBlock));
   const size_t smem = sizeof(float) * 2 * kPkTile * a.head_dim;
