@@ -121,6 +121,11 @@ struct GemmArgs {
 int gemm_splits(int M, int N, int K);
 size_t gemm_ws_floats(int M, int N, int K);
 hipError_t launch_gemm(const GemmArgs &a, GemvEpi epi, hipStream_t s);
+// EPI_RESID GEMM (y += A W^T) followed by the RMSNorm of y with gains g into
+// bf16 hi/lo planes, the split-K reduction and the norm in one pass when the
+// shape allows (else launch_gemm + launch_rmsnorm_rows_split)
+hipError_t launch_gemm_resid_norm(const GemmArgs &a, const uint16_t *g, float eps, uint16_t *hi,
+                                  uint16_t *lo, hipStream_t s);
 
 struct AttnPrefillArgs {
   const float *q;               // [M, nq*d]

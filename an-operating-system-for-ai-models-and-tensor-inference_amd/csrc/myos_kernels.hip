@@ -900,6 +900,59 @@ __global__ void __launch_bounds__(kBlock) gemm_mfma_kernel(GemmArgs a) {
   }
 }
 
+// EPI_RESID's K splits fused with the RMSNorm that reads the result: row r of
+// y += (the splits of row r, added in split order), then the normalised row
+// (gains g) as bf16 hi/lo planes, as rmsnorm_rows_split_kernel writes them.
+// One workgroup per row, NV 4-column groups per thread.
+template <int NV>
+__global__ void __launch_bounds__(kBlock) gemm_resid_norm_kernel(GemmArgs a, int splits,
+                                                                 const uint16_t *g, float eps,
+                                                                 uint16_t *hi, uint16_t *lo) {
+  __shared__ float red4[4];
+  const int r = blockIdx.x, H = a.N, n4 = H >> 2;
+  const size_t MN = (size_t)a.M * H;
+  const float *ws = a.ws + (size_t)r * H;
+  float *y = a.y + (size_t)r * H;
+  float4 xv[NV];
+  float ss = 0.f;
+#pragma unroll
+  for (int v = 0; v < NV; v++) {
+    const int c4 = threadIdx.x + v * kBlock;
+    xv[v] = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (c4 < n4) {
+      float4 c = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll 4
+      for (int z = 0; z < splits; z++) {
+        const float4 w = *(const float4 *)(ws + z * MN + 4 * c4);
+        c.x += w.x;
+        c.y += w.y;
+        c.z += w.z;
+        c.w += w.w;
+      }
+      float4 x = *(const float4 *)(y + 4 * c4);
+      x.x += c.x;
+      x.y += c.y;
+      x.z += c.z;
+      x.w += c.w;
+      *(float4 *)(y + 4 * c4) = x;
+      xv[v] = x;
+      ss += x.x * x.x + x.y * x.y + x.z * x.z + x.w * x.w;
+    }
+  }
+  const float tot = block_sum(ss, red4);
+  const float inv = 1.0f / sqrtf(tot / (float)H + eps);
+#pragma unroll
+  for (int v = 0; v < NV; v++) {
+    const int c4 = threadIdx.x + v * kBlock;
+    if (c4 < n4) {
+      const size_t o = (size_t)r * H + 4 * c4;
+      const float xe[4] = {xv[v].x, xv[v].y, xv[v].z, xv[v].w};
+#pragma unroll
+      for (int e = 0; e < 4; e++) split2(bf16f(g[4 * c4 + e]) * (xe[e] * inv), hi + o + e, lo + o + e);
+    }
+  }
+}
+
 // the K splits of gemm_mfma_kernel, added in split order, then the epilogue;
 // one thread per column pair (a last odd column stands alone)
 template <int EPI>
@@ -1363,14 +1416,45 @@ size_t gemm_ws_floats(int M, int N, int K) {
   return sp > 1 ? (size_t)sp * M * N : 0;
 }
 
-hipError_t launch_gemm(const GemmArgs &args, GemvEpi epi, hipStream_t s) {
-  if (args.M <= 0 || args.N <= 0) return hipSuccess;
-  GemmArgs a = args;
+// the launch shape of a GEMM: K splits (1 when the partial buffer is short)
+// and K steps per split in a.kps
+static int gemm_plan(GemmArgs &a) {
   const int ksteps = (a.K + GBK - 1) / GBK;
   int splits = gemm_splits(a.M, a.N, a.K);
   if (!a.ws || a.ws_cap < (size_t)splits * a.M * a.N) splits = 1;  // no room for partials
   a.kps = (ksteps + splits - 1) / splits;
   if (a.kps < 1) a.kps = 1;
+  return splits;
+}
+
+hipError_t launch_gemm_resid_norm(const GemmArgs &args, const uint16_t *g, float eps,
+                                  uint16_t *hi, uint16_t *lo, hipStream_t s) {
+  if (args.M <= 0 || args.N <= 0) return hipSuccess;
+  GemmArgs a = args;
+  const int splits = gemm_plan(a);
+  const int n4 = a.N >> 2;
+  const bool fused = splits > 1 && (a.N & 3) == 0 && n4 <= 4 * kBlock &&
+                     (((uintptr_t)a.ws | (uintptr_t)a.y) & 15) == 0;
+  if (!fused) {
+    hipError_t e = launch_gemm(args, EPI_RESID, s);
+    if (e != hipSuccess) return e;
+    return launch_rmsnorm_rows_split(a.y, g, eps, a.M, a.N, hi, lo, s);
+  }
+  dim3 grid(nblk((size_t)a.N, GBN), nblk((size_t)a.M, GBM), splits);
+  hipLaunchKernelGGL(gemm_mfma_kernel<EPI_RESID>, grid, dim3(kBlock), 0, s, a);
+  if (n4 <= kBlock)
+    hipLaunchKernelGGL(gemm_resid_norm_kernel<1>, dim3(a.M), dim3(kBlock), 0, s, a, splits, g, eps, hi, lo);
+  else if (n4 <= 2 * kBlock)
+    hipLaunchKernelGGL(gemm_resid_norm_kernel<2>, dim3(a.M), dim3(kBlock), 0, s, a, splits, g, eps, hi, lo);
+  else
+    hipLaunchKernelGGL(gemm_resid_norm_kernel<4>, dim3(a.M), dim3(kBlock), 0, s, a, splits, g, eps, hi, lo);
+  return hipGetLastError();
+}
+
+hipError_t launch_gemm(const GemmArgs &args, GemvEpi epi, hipStream_t s) {
+  if (args.M <= 0 || args.N <= 0) return hipSuccess;
+  GemmArgs a = args;
+  const int splits = gemm_plan(a);
   dim3 grid(nblk((size_t)a.N, GBN), nblk((size_t)a.M, GBM), splits);
   const unsigned rgrid = nblk((size_t)a.M * ((a.N + 1) >> 1), kBlock);
   switch (epi) {

@@ -854,9 +854,10 @@ int myos_prefill(myos_model *m, const uint32_t *tokens, size_t n) {
   HIP_TRY(hipMemcpyAsync(m->ptok, tokens, n * 4, hipMemcpyHostToDevice, st));
   HIP_TRY(hipEventRecord(m->ev0, st));
   HIP_TRY(launch_embed_rows(m->pX, m->embed, m->ptok, M, H, st));
+  // layer 0's ln1 here; every later norm rides on the GEMM before it
+  HIP_TRY(launch_rmsnorm_rows_split(m->pX, m->layers[0].ln1, s.rms_eps, M, H, m->pAhi, m->pAlo, st));
   for (size_t l = 0; l < s.num_layers; l++) {
     const DevLayer &L = m->layers[l];
-    HIP_TRY(launch_rmsnorm_rows_split(m->pX, L.ln1, s.rms_eps, M, H, m->pAhi, m->pAlo, st));
     GemmArgs g{};
     g.a_hi = m->pAhi;
     g.a_lo = m->pAlo;
@@ -904,9 +905,8 @@ int myos_prefill(myos_model *m, const uint32_t *tokens, size_t n) {
     o.y = m->pX;
     o.ws = m->pws;
     o.ws_cap = m->pws_cap;
-    HIP_TRY(launch_gemm(o, EPI_RESID, st));
+    HIP_TRY(launch_gemm_resid_norm(o, L.ln2, s.rms_eps, m->pAhi, m->pAlo, st));
 
-    HIP_TRY(launch_rmsnorm_rows_split(m->pX, L.ln2, s.rms_eps, M, H, m->pAhi, m->pAlo, st));
     GemmArgs gu{};
     gu.a_hi = m->pAhi;
     gu.a_lo = m->pAlo;
@@ -930,7 +930,10 @@ int myos_prefill(myos_model *m, const uint32_t *tokens, size_t n) {
     dn.y = m->pX;
     dn.ws = m->pws;
     dn.ws_cap = m->pws_cap;
-    HIP_TRY(launch_gemm(dn, EPI_RESID, st));
+    if (l + 1 < s.num_layers)
+      HIP_TRY(launch_gemm_resid_norm(dn, m->layers[l + 1].ln1, s.rms_eps, m->pAhi, m->pAlo, st));
+    else
+      HIP_TRY(launch_gemm(dn, EPI_RESID, st));
   }
   const float *last = m->pX + (size_t)(M - 1) * H;
   HIP_TRY(hipMemcpyAsync(m->x, last, (size_t)H * 4, hipMemcpyDeviceToDevice, st));
