@@ -953,6 +953,29 @@ __global__ void __launch_bounds__(kBlock) gemm_resid_norm_kernel(GemmArgs a, int
   }
 }
 
+// gemm_reduce_kernel for N % 4 == 0: one thread per two column pairs, float4 loads
+template <int EPI>
+__global__ void __launch_bounds__(kBlock) gemm_reduce4_kernel(GemmArgs a, int splits) {
+  const int n4 = a.N >> 2;
+  const size_t i = blockIdx.x * (size_t)kBlock + threadIdx.x;
+  if (i >= (size_t)a.M * n4) return;
+  const int row = (int)(i / (size_t)n4), col = 4 * (int)(i % (size_t)n4);
+  const size_t MN = (size_t)a.M * a.N, off = (size_t)row * a.N + col;
+  float4 c = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll 4
+  for (int z = 0; z < splits; z++) {
+    const float4 w = *(const float4 *)(a.ws + z * MN + off);
+    c.x += w.x;
+    c.y += w.y;
+    c.z += w.z;
+    c.w += w.w;
+  }
+  gemm_store<EPI>(a, row, col, c.x, c.y);
+  gemm_store<EPI>(a, row, col + 1, c.y, c.x);
+  gemm_store<EPI>(a, row, col + 2, c.z, c.w);
+  gemm_store<EPI>(a, row, col + 3, c.w, c.z);
+}
+
 // the K splits of gemm_mfma_kernel, added in split order, then the epilogue;
 // one thread per column pair (a last odd column stands alone)
 template <int EPI>
@@ -1457,11 +1480,15 @@ hipError_t launch_gemm(const GemmArgs &args, GemvEpi epi, hipStream_t s) {
   const int splits = gemm_plan(a);
   dim3 grid(nblk((size_t)a.N, GBN), nblk((size_t)a.M, GBM), splits);
   const unsigned rgrid = nblk((size_t)a.M * ((a.N + 1) >> 1), kBlock);
+  const bool r4 = (a.N & 3) == 0 && ((uintptr_t)a.ws & 15) == 0;
+  const unsigned rgrid4 = nblk((size_t)a.M * (a.N >> 2), kBlock);
   switch (epi) {
 #define MYOS_GEMM_CASE(E)                                                          \
   case E:                                                                         \
     hipLaunchKernelGGL(gemm_mfma_kernel<E>, grid, dim3(kBlock), 0, s, a);         \
-    if (splits > 1)                                                               \
+    if (splits > 1 && r4)                                                         \
+      hipLaunchKernelGGL(gemm_reduce4_kernel<E>, dim3(rgrid4), dim3(kBlock), 0, s, a, splits); \
+    else if (splits > 1)                                                          \
       hipLaunchKernelGGL(gemm_reduce_kernel<E>, dim3(rgrid), dim3(kBlock), 0, s, a, splits); \
     break;
     MYOS_GEMM_CASE(EPI_STORE)
