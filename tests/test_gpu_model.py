@@ -5,6 +5,7 @@
 * the chunk-prefill fixture (rich_map, qwen25_block.rs:1423-1478): the GPU's
   MFMA prefill and its GEMV forward_token both agree with the oracle;
 * seeded random small models, f32 and bf16 KV;
+* prefill attention with and without key groups, for head_dim 32, 64, 128;
 * the Qwen2.5-1.5B shape: prompt [0] + 4 greedy steps, and 128 prompt ids +
   teacher-forced decode, under the tolerance rule in parity.py.
 """
@@ -148,6 +149,29 @@ def test_random_small_models(tmp_path, kv, dims):
         assert max_rel(g.logits(), o.logits()) < tol, step
         if kv == myos.KV_F32:
             assert_logits_parity(g.logits(), o.logits(), f"step {step}")
+    g.close()
+
+
+# Prefill attention runs four key groups per workgroup when the (q head,
+# 16-query) grid is smaller than the 256 CUs and one group otherwise: each
+# head_dim, at a prompt length on either side of that line (nq * ceil(M / 16)
+# against 256), against the oracle.
+@pytest.mark.parametrize("dims,m", [((384, 12, 2, 32, 1000, 4099, 2), 40),
+                                    ((384, 12, 2, 32, 1000, 4099, 2), 400),
+                                    ((256, 4, 2, 64, 512, 1000, 2), 40),
+                                    ((256, 4, 2, 64, 512, 1000, 2), 1100),
+                                    ((512, 4, 1, 128, 1536, 2048, 2), 40),
+                                    ((512, 4, 1, 128, 1536, 2048, 2), 1100)])
+def test_prefill_attention_key_groups(tmp_path, dims, m):
+    s = shape_dict(*dims, 1e-6)
+    t = random_map(s, seed=sum(dims) + m, std=0.05)
+    g, o = open_pair(tmp_path, s, t, m + 8)
+    prompt = np.random.default_rng(m).integers(0, s["vocab"], m)
+    g.prefill(prompt)
+    assert o.prefill(prompt) == 0
+    assert max_rel(g.logits(), o.logits()) < 1e-4
+    assert max_rel(g.hidden(), o.hidden()) < 1e-4
+    assert_logits_parity(g.logits(), o.logits(), f"prefill of {m} ids")
     g.close()
 
 
