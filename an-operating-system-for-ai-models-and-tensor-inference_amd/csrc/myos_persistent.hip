@@ -513,8 +513,9 @@ __host__ __device__ inline int gu_share(int I, int nkv, int nchmax, int nq, int 
 // the launch arguments: the launcher picks the Qwen2.5-1.5B instantiation for
 // that shape, where folding the dimensions frees the scalar registers that
 // the generic build would spill, and the generic one for every other shape.
-// KB: the KV cache holds bf16 (else f32).
-template <int kH, int kI, int kV, int kNQ, int kNKV, int kD, bool KB>
+// KB: the KV cache holds bf16 (else f32). MS: more than 16 attention chunks
+// per head (max_seq > 512), each head's merge split over four workgroups.
+template <int kH, int kI, int kV, int kNQ, int kNKV, int kD, bool KB, bool MS>
 __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
   extern __shared__ float4 sm4[];
   float *xs = (float *)sm4;     // [MAXH] activation for the current phase
@@ -892,30 +893,42 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
 
       // ---- merge: q head h's chunks -> att[h] (tag T + P_ATT), on the last
       // workgroups (attention items start at the first); one wave combines
-      // att = sum_c e^(m_c - M) o_c / sum_c e^(m_c - M) l_c ----------------
-      const int mh = NB - 1 - wg;
+      // att = sum_c e^(m_c - M) o_c / sum_c e^(m_c - M) l_c. Launches with
+      // more than 16 chunks per head (MS) split a head over four workgroups of
+      // d / 4 columns each, so no merge gathers more than about 5 words a thread.
+      constexpr int mp = MS ? 4 : 1;
+      const int mi = NB - 1 - wg, mh = mi / mp, mq = mi - mh * mp;
       if (mh < nq) {
-        const int dd = d + 2;
-        float *pc = big;                     // [nch][d + 2] gathered partials
-        float *wc = big + nch * dd;          // [nch] chunk weights
+        const int dd = d + 2, dw = d / mp, dpw = dw + 2, j0 = mq * dw;
+        float *pc = big;                     // [nch][dw + 2]: columns j0 .. j0 + dw, then m, l
+        float *wc = big + nch * dpw;         // [nch] chunk weights
         const int base = mh * nchmax * dd;
-        tgather<2>(a.tpart, [base](int i) { return base + i; }, nch * dd, T + P_PART, pc, a, &fail_s);
+        if (!MS)
+          tgather<2>(a.tpart, [base](int i) { return base + i; }, nch * dd, T + P_PART, pc, a, &fail_s);
+        else
+          tgather<2>(
+              a.tpart,
+              [base, dd, dw, dpw, j0, d](int i) {
+                const int c = i / dpw, r = i - c * dpw;
+                return base + c * dd + (r < dw ? j0 + r : d + (r - dw));
+              },
+              nch * dpw, T + P_PART, pc, a, &fail_s);
         if (wave == 0) {
           float mloc = -INFINITY;
-          for (int c = lane; c < nch; c += 64) mloc = fmaxf(mloc, pc[c * dd + d]);
+          for (int c = lane; c < nch; c += 64) mloc = fmaxf(mloc, pc[c * dpw + dw]);
           const float mx = wave_max(mloc);
           float lloc = 0.f;
           for (int c = lane; c < nch; c += 64) {
-            const float e = expf(pc[c * dd + d] - mx);
+            const float e = expf(pc[c * dpw + dw] - mx);
             wc[c] = e;
-            lloc = fmaf(e, pc[c * dd + d + 1], lloc);
+            lloc = fmaf(e, pc[c * dpw + dw + 1], lloc);
           }
           const float inv = 1.0f / wave_sum(lloc);
-          for (int j = lane; j < d; j += 64) {
+          for (int j = lane; j < dw; j += 64) {
             float acc = 0.f;
 #pragma unroll 4
-            for (int c = 0; c < nch; c++) acc = fmaf(wc[c], pc[c * dd + j], acc);
-            tput(a.tatt + mh * d + j, acc * inv, T + P_ATT);
+            for (int c = 0; c < nch; c++) acc = fmaf(wc[c], pc[c * dpw + j], acc);
+            tput(a.tatt + mh * d + j0 + j, acc * inv, T + P_ATT);
           }
         }
         __syncthreads();
@@ -1222,14 +1235,19 @@ hipError_t launch_decode_persistent(const PersistArgs &a, hipStream_t s) {
   const bool qwen15 = a.H == 1536 && a.I == 8960 && a.V == 151936 && a.nq == 12 && a.nkv == 2 &&
                       a.d == 128;
   const bool kb = a.kv_bf16 != 0;
-  const void *const fns[4] = {
-      (const void *)decode_persistent_kernel<0, 0, 0, 0, 0, 0, false>,
-      (const void *)decode_persistent_kernel<0, 0, 0, 0, 0, 0, true>,
-      (const void *)decode_persistent_kernel<1536, 8960, 151936, 12, 2, 128, false>,
-      (const void *)decode_persistent_kernel<1536, 8960, 151936, 12, 2, 128, true>};
-  const int which = 2 * qwen15 + kb;
+  const bool ms = (a.max_seq + AC - 1) / AC > 16;
+  const void *const fns[8] = {
+      (const void *)decode_persistent_kernel<0, 0, 0, 0, 0, 0, false, false>,
+      (const void *)decode_persistent_kernel<0, 0, 0, 0, 0, 0, true, false>,
+      (const void *)decode_persistent_kernel<1536, 8960, 151936, 12, 2, 128, false, false>,
+      (const void *)decode_persistent_kernel<1536, 8960, 151936, 12, 2, 128, true, false>,
+      (const void *)decode_persistent_kernel<0, 0, 0, 0, 0, 0, false, true>,
+      (const void *)decode_persistent_kernel<0, 0, 0, 0, 0, 0, true, true>,
+      (const void *)decode_persistent_kernel<1536, 8960, 151936, 12, 2, 128, false, true>,
+      (const void *)decode_persistent_kernel<1536, 8960, 151936, 12, 2, 128, true, true>};
+  const int which = 4 * ms + 2 * qwen15 + kb;
   const void *fn = fns[which];
-  static bool attr_set[4] = {false, false, false, false};
+  static bool attr_set[8] = {false, false, false, false, false, false, false, false};
   if (!attr_set[which]) {
     hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxLds);
     if (e != hipSuccess) return e;

@@ -157,6 +157,36 @@ def test_persistent_bf16_cache(tmp_path, dims, persist_kernel):
     k.close()
 
 
+@pytest.mark.parametrize("dims", [SMALL[0], SMALL[3]])
+def test_persistent_split_merge(tmp_path, dims, persist_kernel):
+    """max_seq 600 gives 19 attention chunks per head: the first kernel then
+    merges each head on four workgroups of head_dim / 4 columns. Prompt of 530
+    ids, 40 greedy steps, against the oracle."""
+    if persist_kernel == "stream":
+        pytest.skip("the streamed kernel merges per head on one wave")
+    s = shape_dict(*dims, 1e-6)
+    t = random_map(s, seed=sum(dims) + 5, std=0.05)
+    path = str(tmp_path / "m.safetensors")
+    write_safetensors(path, t)
+    max_seq = 600
+    g = myos.Model.open(path, to_block_shape(s), myos.KV_F32, max_seq)
+    if g.decode_path() != myos.DECODE_PERSISTENT:
+        g.close()
+        pytest.skip("the device cannot hold the cooperative decode grid")
+    o = oracle.Model(s, t, max_seq, threads=4)
+    prompt = np.random.default_rng(13).integers(0, s["vocab"], 530)
+    g.prefill(prompt)
+    assert o.prefill(prompt) == 0
+    ids_g = g.greedy_decode(40)
+    ids_o, gaps = oracle_steps(o, 40)
+    n_ok = agree(ids_g, ids_o, gaps)
+    assert g.cache_len() == 570
+    if n_ok == 40:
+        assert_logits_parity(g.logits(), o.logits(), "split merge, after 40 steps")
+        assert max_rel(g.hidden(), o.hidden()) < 1e-4
+    g.close()
+
+
 def test_persistent_until_cache_full(tmp_path):
     s = shape_dict(256, 4, 2, 64, 512, 1000, 2, 1e-6)
     t = random_map(s, seed=5, std=0.05)
