@@ -159,7 +159,7 @@ struct PersistArgs {
   float *kc, *vc;              // f32 cache base, layer stride = layer_kv
   size_t layer_kv;
   // tagged exchange buffers (zeroed once; tags only grow)
-  uint64_t *tq, *tkv, *tpart, *tatt, *txo, *th, *txd, *targ;
+  uint64_t *tq, *tkv, *tpart, *tatt, *txo, *txd, *targ;
   uint64_t *tpd;               // streamed kernel: [grid][H] down partials per workgroup
   uint64_t *tpr;               // first kernel: down partials, [owner][grid][rows per owner]
   int ring_slots;              // streamed kernel: set by the launcher
@@ -172,7 +172,7 @@ struct PersistArgs {
   uint32_t *state, *out_ids;
   uint32_t *err;
   uint32_t tag_base, steps, pos0;
-  int lds_wd;                  // set by the launcher: LDS offset (floats) of the down rows
+  int lds_wd;                  // set by the launcher: LDS offset (floats) of the down block
   int kv_bf16;                 // the cache at kc / vc holds bf16 (first kernel only)
   uint64_t *trace;             // optional [grid][5 L + 3] phase timestamps of one step
   uint32_t trace_step;

@@ -435,11 +435,10 @@ int setup_persistent(myos_model *m) {
   a.tpr = nullptr;
   m->persist_stream = want_stream && stream_device_ok(a);
   if (!m->persist_stream && !persist_device_ok(a)) return MYOS_OK;
-  const size_t words[10] = {m->q_dim, 2 * m->kv_dim,
-                            std::max(persist_part_words(a.nq, a.max_seq, a.d),
-                                     stream_part_words(a.nq, a.max_seq, a.d)),
-                            m->q_dim, s.hidden,
-                            s.intermediate, s.hidden, 2 * (size_t)persist_grid(),
+  const size_t words[9] = {m->q_dim, 2 * m->kv_dim,
+                           std::max(persist_part_words(a.nq, a.max_seq, a.d),
+                                    stream_part_words(a.nq, a.max_seq, a.d)),
+                           m->q_dim, s.hidden, s.hidden, 2 * (size_t)persist_grid(),
                             m->persist_stream ? stream_tpd_words((int)s.hidden) : 0,
                             m->persist_stream ? 0
                                               : (size_t)persist_grid() * persist_grid() *
@@ -450,10 +449,9 @@ int setup_persistent(myos_model *m) {
   HIP_TRY(hipMalloc((void **)&m->pbuf, total));
   HIP_TRY(hipMemsetAsync(m->pbuf, 0, total, m->stream));
   m->pbuf_bytes = total;
-  uint64_t **dst[10] = {&a.tq,  &a.tkv, &a.tpart, &a.tatt, &a.txo,
-                        &a.th,  &a.txd, &a.targ,  &a.tpd,  &a.tpr};
+  uint64_t **dst[9] = {&a.tq, &a.tkv, &a.tpart, &a.tatt, &a.txo, &a.txd, &a.targ, &a.tpd, &a.tpr};
   uint8_t *p = m->pbuf;
-  for (int i = 0; i < 10; i++) {
+  for (int i = 0; i < 9; i++) {
     *dst[i] = (uint64_t *)p;
     p += align256(words[i] * 8);
   }

@@ -146,10 +146,6 @@ __device__ bool tgather(const uint64_t *src, Map map, int n, uint32_t tag, float
   return *fail == 0;
 }
 
-struct Linear {
-  __device__ int operator()(int i) const { return i; }
-};
-
 // tgather for src[0, n) in order: one buffer descriptor, one lane offset and
 // per-unroll constant offsets keep the address cost at one register. The
 // loads are sc1 (device-coherent) and volatile, so a spin re-reads memory.
@@ -908,7 +904,7 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
         else
           tgather<2>(
               a.tpart,
-              [base, dd, dw, dpw, j0, d](int i) {
+              [=](int i) {
                 const int c = i / dpw, r = i - c * dpw;
                 return base + c * dd + (r < dw ? j0 + r : d + (r - dw));
               },
