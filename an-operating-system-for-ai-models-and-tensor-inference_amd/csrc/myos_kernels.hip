@@ -1428,6 +1428,8 @@ int gemm_splits(int M, int N, int K) {
   // about two workgroups per CU, so one's operand loads overlap the other's
   // MFMAs (measured at M = 128: one per CU 4 % slower, three 11 % slower)
   int sp = (512 + tiles - 1) / tiles;
+  // partials (sp M N f32) no larger than the weights (N K bf16)
+  if (sp > K / (2 * M)) sp = K / (2 * M);
   if (sp > ksteps) sp = ksteps;
   if (sp < 1) sp = 1;
   const int kps = (ksteps + sp - 1) / sp;
