@@ -1203,6 +1203,8 @@ static size_t persist_lds(PersistArgs &a) {
   if ((size_t)np > big) big = np;
   const size_t xper = (size_t)(a.H + NB - 1) / NB;
   if (64 + NB * xper > big) big = 64 + NB * xper;  // h share, then the down partials
+  // the h share sits in the 64 floats before the gathered partials (np is at
+  // most GPMAX * NW = 40 on every supported shape; larger would not fit)
   if (np > 64) return kMaxLds + 1;
   const size_t wd_off = 2 * MAXH + ((big + 3) & ~(size_t)3);  // floats
   a.lds_wd = (int)wd_off;
