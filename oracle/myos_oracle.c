@@ -582,6 +582,27 @@ int orc_forward_token(orc_model *m, uint32_t token, size_t pos) {
   return ORC_OK;
 }
 
+/* attend_chunk's per-position loop (qwen25_block.rs:737-756): positions are
+ * independent and each is the serial gqa_attn_f32, so spreading them over the
+ * pool changes no bit; every part has its own probs scratch. */
+typedef struct {
+  orc_model *m;
+  float *A;
+  const float *Q;
+  size_t n, start, end;
+  float *probs; /* [nparts][end] */
+} attend_job;
+
+static void attend_part(void *p, int part, int nparts) {
+  attend_job *j = (attend_job *)p;
+  orc_model *m = j->m;
+  size_t qd = m->q_dim, d = m->s.head_dim;
+  float *probs = j->probs + (size_t)part * j->end;
+  for (size_t i = (size_t)part; i < j->n; i += (size_t)nparts)
+    orc_gqa_attn_f32(j->A + i * qd, j->Q + i * qd, m->pack_k, m->pack_v, probs,
+                     m->s.num_q_heads, m->s.num_kv_heads, d, j->end, 1, j->start + i);
+}
+
 /* prefill, crates/model_core/src/qwen25_block.rs:323-543 */
 int orc_prefill(orc_model *m, const uint32_t *tokens, size_t n) {
   if (n == 0) return ORC_E_SHAPE;
@@ -615,9 +636,12 @@ int orc_prefill(orc_model *m, const uint32_t *tokens, size_t n) {
     }
     /* attend_chunk, qwen25_block.rs:714-758 */
     kv_pack(m, l, end);
-    for (size_t i = 0; i < n; i++)
-      orc_gqa_attn_f32(A + i * qd, Q + i * qd, m->pack_k, m->pack_v, m->probs,
-                       m->s.num_q_heads, m->s.num_kv_heads, d, end, 1, start + i);
+    {
+      int parts = n < 8 ? 1 : m->threads;
+      attend_job job = {m, A, Q, n, start, end, zalloc((size_t)parts * end)};
+      pool_run(attend_part, &job, parts);
+      free(job.probs);
+    }
     orc_gemm_bf16_mt(P, L->wo, A, n, H, qd, m->threads);
     for (size_t i = 0; i < n; i++) add_assign(X + i * H, P + i * H, H);
     for (size_t i = 0; i < n; i++)

@@ -90,16 +90,47 @@ def block_fixture_layer(t, layer, q_b, v_b, o_w, gate, up, down):
     t[p + "mlp.down_proj.weight"] = bits(down, (2, 2))
 
 
-def block_fixture():
-    """block_fixture, qwen25_block.rs:811-840: token 0 -> logits [1, 2, 0, -1]."""
-    t = {
-        "model.embed_tokens.weight": bits([1.0, 1.0, 2.0, 0.0, 0.0, 4.0, -1.0, 0.0], (4, 2)),
-        "model.norm.weight": bits([1.0, 0.0]),
+FIXTURE_EMBED = [1.0, 1.0, 2.0, 0.0, 0.0, 4.0, -1.0, 0.0]
+
+
+def fixture_embed_and_final(final_gamma=(1.0, 0.0)):
+    """insert_embed_and_final, qwen25_block.rs:828-840: embed rows [1,1], [2,0],
+    [0,4], [-1,0]; final gamma [1, 0]."""
+    return {
+        "model.embed_tokens.weight": bits(FIXTURE_EMBED, (4, 2)),
+        "model.norm.weight": bits(list(final_gamma)),
     }
+
+
+def block_fixture():
+    """block_fixture, qwen25_block.rs:811-826: token 0 -> logits [1, 2, 0, -1]."""
+    t = fixture_embed_and_final()
     block_fixture_layer(t, 0, [0.5, 0.0, 0.0, 0.25], [1.0, 0.0],
                         [1.0, 0.0, 0.0, 0.0, 1.0, 0.0, 0.0, 0.0], [0.0] * 4, [0.0] * 4,
                         [0.0] * 4)
     return fixture_shape(), t
+
+
+def swiglu_residual_fixture():
+    """swiglu_residual_changes_the_logits, qwen25_block.rs:1074-1129: the block
+    fixture with gate = up = [[1, 0], [0, 0]] and down = identity, so the MLP
+    adds [silu(1), 0] to the stream [2, 2]."""
+    t = fixture_embed_and_final()
+    block_fixture_layer(t, 0, [0.5, 0.0, 0.0, 0.25], [1.0, 0.0],
+                        [1.0, 0.0, 0.0, 0.0, 1.0, 0.0, 0.0, 0.0], [1.0, 0.0, 0.0, 0.0],
+                        [1.0, 0.0, 0.0, 0.0], [1.0, 0.0, 0.0, 1.0])
+    return fixture_shape(), t
+
+
+def two_layer_fixture():
+    """two_layers_advance_once_per_token, qwen25_block.rs:1132-1197: o_proj and
+    the MLP are zero in both layers; V biases [2, 0] (layer 0) and [0, 8]
+    (layer 1), stored at the same cursor."""
+    t = fixture_embed_and_final()
+    zero_o, zero_mlp = [0.0] * 8, [0.0] * 4
+    block_fixture_layer(t, 0, [0.0] * 4, [2.0, 0.0], zero_o, zero_mlp, zero_mlp, zero_mlp)
+    block_fixture_layer(t, 1, [0.0] * 4, [0.0, 8.0], zero_o, zero_mlp, zero_mlp, zero_mlp)
+    return fixture_shape(2), t
 
 
 # ------------------------------------------------------------- rich map ----

@@ -390,6 +390,167 @@ def test_block_errors_do_not_advance(orc):
     assert small.prefill([0, 0, 0]) == 5 and small.cache_len() == 0
 
 
+def _rms_f32(x, gamma, eps):
+    """RMSNorm in the reference's f32 order (bf16.rs:243-270): serial sum of
+    squares, mean, 1/sqrt(mean + eps), g * (x * inv)."""
+    x = np.asarray(x, np.float32)
+    s = np.float32(0)
+    for v in x:
+        s = np.float32(s + np.float32(v * v))
+    inv = np.float32(1) / np.float32(math.sqrt(np.float32(s / np.float32(len(x)) + eps)))
+    return np.asarray([np.float32(g * np.float32(v * inv)) for g, v in zip(gamma, x)],
+                      np.float32)
+
+
+def _fixture_head(normed):
+    """Tied head of the fixture embedding rows [1,1], [2,0], [0,4], [-1,0]."""
+    n0, n1 = np.float32(normed[0]), np.float32(normed[1])
+    rows = [(1, 1), (2, 0), (0, 4), (-1, 0)]
+    return [np.float32(np.float32(np.float32(a) * n0) + np.float32(np.float32(b) * n1))
+            for a, b in rows]
+
+
+def test_swiglu_residual_changes_the_logits(orc):
+    # qwen25_block.rs:1074-1129: the stream is [2, 2] before the MLP, its
+    # post-norm [1, 1]; gate and up read lane 0, so h = [silu(1) * 1, 0] and
+    # down (identity) adds [silu(1), 0]. silu(1) = 0x3F3B26A8 (swiglu.rs:362-377).
+    from model_fixtures import swiglu_residual_fixture
+    s, t = swiglu_residual_fixture()
+    silu1 = np.uint32(0x3F3B26A8).view(np.float32)
+    residual = [np.float32(2.0 + silu1), np.float32(2.0)]
+    expect = _fixture_head(_rms_f32(residual, [1.0, 0.0], np.float32(0)))
+    assert expect != [1.0, 2.0, 0.0, -1.0]
+    m = orc.Model(s, t, 2, threads=1)
+    assert m.forward_token(0, 0) == 0
+    assert fbits(m.logits()) == fbits(expect)
+    assert fbits(m.hidden()) == fbits(residual)
+    assert m.cache_len() == 1
+    assert list(m.kv(0, 0, 0)[1]) == [1.0, 0.0]
+    # the prefill chunk path gives the same bits
+    mp = orc.Model(s, t, 2, threads=1)
+    assert mp.prefill([0]) == 0 and fbits(mp.logits()) == fbits(expect)
+
+
+def test_two_layers_advance_once_per_token(orc):
+    # qwen25_block.rs:1132-1197
+    from model_fixtures import two_layer_fixture
+    s, t = two_layer_fixture()
+    for use_prefill in (False, True):
+        m = orc.Model(s, t, 4, threads=1)
+        if use_prefill:
+            assert m.prefill([0]) == 0
+        else:
+            assert m.forward_token(0, 0) == 0
+        assert list(m.logits()) == [1.0, 2.0, 0.0, -1.0]
+        assert m.cache_len() == 1
+        assert list(m.kv(0, 0, 0)[1]) == [2.0, 0.0] and list(m.kv(1, 0, 0)[1]) == [0.0, 8.0]
+        assert list(m.kv(0, 0, 0)[0]) == [0.0, 0.0] and list(m.kv(1, 0, 0)[0]) == [0.0, 0.0]
+        assert list(m.kv(0, 0, 1)[1]) == [0.0, 0.0] and list(m.kv(1, 0, 1)[1]) == [0.0, 0.0]
+        assert m.forward_token(1, 1) == 0
+        assert m.cache_len() == 2
+        assert list(m.kv(0, 0, 0)[1]) == [2.0, 0.0] and list(m.kv(1, 0, 0)[1]) == [0.0, 8.0]
+        assert list(m.kv(0, 0, 1)[1]) == [2.0, 0.0] and list(m.kv(1, 0, 1)[1]) == [0.0, 8.0]
+        # token 1 embeds to [2, 0]; attention and SwiGLU add 0; final gamma [1, 0]
+        expect = _fixture_head(_rms_f32([2.0, 0.0], [1.0, 0.0], np.float32(0)))
+        assert fbits(m.logits()) == fbits(expect)
+        assert expect[1] > expect[0] and orc.greedy_token(m.logits()) == 1
+
+
+def test_post_attention_norm_feeds_the_mlp(orc):
+    # Closed form on the fixture shape, chosen so that the plausible wiring
+    # mistakes give different logits: ln2 gamma [2, 0] (ln1 stays [1, 1]), so
+    # the MLP input is rms([2, 2]) * [2, 0] = [2, 0], not the ln1-normed [1, 1];
+    # gate = [[1,0],[0,0]], up = identity: h = [silu(2) * 2, 0] with
+    # silu(2) = 0x3FE17BEA (swiglu.rs:362-377); down = [[1,0],[0.5,0]] adds
+    # [h0, h0 / 2] to the stream; final gamma [1, 0.5].
+    from model_fixtures import block_fixture_layer, fixture_embed_and_final
+    s = fixture_shape()
+    t = fixture_embed_and_final((1.0, 0.5))
+    block_fixture_layer(t, 0, [0.0] * 4, [1.0, 0.0], [1.0, 0.0, 0.0, 0.0, 1.0, 0.0, 0.0, 0.0],
+                        [1.0, 0.0, 0.0, 0.0], [1.0, 0.0, 0.0, 1.0], [1.0, 0.0, 0.5, 0.0])
+    t["model.layers.0.post_attention_layernorm.weight"] = bits([2.0, 0.0])
+    silu2 = np.uint32(0x3FE17BEA).view(np.float32)
+    n2 = _rms_f32([2.0, 2.0], [2.0, 0.0], np.float32(0))
+    assert list(n2) == [2.0, 0.0]
+    h0 = np.float32(silu2 * np.float32(2.0))
+    x = [np.float32(2.0 + h0), np.float32(2.0 + np.float32(0.5 * h0))]
+    expect = _fixture_head(_rms_f32(x, [1.0, 0.5], np.float32(0)))
+    m = orc.Model(s, t, 2, threads=1)
+    assert m.forward_token(0, 0) == 0
+    assert fbits(m.hidden()) == fbits(x)
+    assert fbits(m.logits()) == fbits(expect)
+    # the wrong wirings: MLP on the ln1-normed [1, 1], or no MLP residual
+    silu1 = np.uint32(0x3F3B26A8).view(np.float32)
+    wrong = [_fixture_head(_rms_f32([2.0 + silu1, 2.0 + 0.5 * silu1], [1.0, 0.5], 0.0)),
+             _fixture_head(_rms_f32([2.0, 2.0], [1.0, 0.5], 0.0))]
+    assert all(fbits(w) != fbits(expect) for w in wrong)
+
+
+def test_untied_head_copy_equals_tied(orc):
+    # An lm_head.weight equal to the embedding gives bit-identical logits to
+    # the tied head (the 7B checkpoint's untied head is the same GEMV over a
+    # different matrix); a different lm_head moves them.
+    from model_fixtures import random_map, shape_dict
+    s = shape_dict(64, 4, 2, 16, 96, 50, 2, 1e-6)
+    t = random_map(s, seed=3, std=0.1)
+    tied = orc.Model(s, t, 8, threads=1)
+    tu = dict(t)
+    tu["lm_head.weight"] = np.array(t["model.embed_tokens.weight"], copy=True)
+    untied = orc.Model(s, tu, 8, threads=1)
+    td = dict(t)
+    td["lm_head.weight"] = random_map(s, seed=4, std=0.1)["model.embed_tokens.weight"]
+    other = orc.Model(s, td, 8, threads=1)
+    for m in (tied, untied, other):
+        assert m.prefill([5, 7, 9]) == 0
+        assert m.forward_token(11, 3) == 0
+    assert fbits(untied.logits()) == fbits(tied.logits())
+    assert fbits(other.hidden()) == fbits(tied.hidden())
+    assert fbits(other.logits()) != fbits(tied.logits())
+    from qwen2_textbook import Textbook
+    tb = Textbook(s, td)
+    for tok in (5, 7, 9, 11):
+        lg, _, _ = tb.forward(tok)
+    assert np.max(np.abs(other.logits() - lg)) / np.max(np.abs(lg)) < 1e-5
+
+
+@pytest.mark.parametrize("dims,seed", [((32, 4, 2, 8, 48, 40, 3), 1),
+                                       ((48, 6, 1, 8, 64, 33, 2), 2),
+                                       ((64, 4, 4, 16, 80, 50, 4), 3)])
+def test_oracle_matches_textbook_forward(orc, dims, seed):
+    # The oracle's f32 composition against the independent f64 forward on
+    # random models with random (not unit) norm gains, so ln1 / ln2 / final
+    # mix-ups, a dropped residual or a wrong layer's cache would all show.
+    from model_fixtures import random_map, rne_bf16, shape_dict
+    from qwen2_textbook import Textbook
+    s = shape_dict(*dims, 1e-6)
+    t = random_map(s, seed=seed, std=0.2)
+    rng = np.random.default_rng(seed + 100)
+    for name in t:
+        if name.endswith("norm.weight"):
+            t[name] = rne_bf16(rng.uniform(0.5, 1.5, t[name].shape).astype(np.float32))
+    tb = Textbook(s, t)
+    m = orc.Model(s, t, 16, threads=2)
+    prompt = [int(v) for v in rng.integers(0, s["vocab"], 5)]
+    assert m.prefill(prompt) == 0
+    for tok in prompt:
+        lg, hid, nrm = tb.forward(tok)
+    rel = lambda a, b: float(np.max(np.abs(a - b)) / np.max(np.abs(b)))
+    assert rel(m.logits(), lg) < 1e-5 and rel(m.hidden(), hid) < 1e-5
+    assert rel(m.normed(), nrm) < 1e-5
+    for step in range(6):
+        tok = int(np.argmax(lg))
+        assert m.forward_token(tok, m.cache_len()) == 0
+        lg, hid, _ = tb.forward(tok)
+        assert rel(m.logits(), lg) < 1e-5, step
+        assert rel(m.hidden(), hid) < 1e-5, step
+    for l in range(s["num_layers"]):
+        for h in range(s["num_kv_heads"]):
+            for p in (0, 4, 10):
+                k, v = m.kv(l, h, p)
+                kt, vt = tb.kv(l, h, p)
+                assert rel(k, kt) < 1e-5 and rel(v, vt) < 1e-5, (l, h, p)
+
+
 def _serial(m, tokens, start):
     last = None
     for i, tok in enumerate(tokens):
