@@ -90,6 +90,8 @@ EXPORTS = {
     "myos_decode_path": ([P], I32),
     "myos_set_decode_trace": ([P, C.c_int64], I32),
     "myos_copy_decode_trace": ([P, P, SZ], I32),
+    "myos_debug_raise_wait_error": ([P], I32),
+    "myos_decode_forced": ([P, P, SZ, P], I32),
     "myos_last_prefill_ms": ([P], C.c_double),
     "myos_last_decode_ms": ([P], C.c_double),
     "myos_weight_bytes": ([P], SZ),
@@ -321,6 +323,20 @@ class Model:
             err.partial = [int(v) for v in out[:self.cache_len() - before]]
             raise err
         return [int(v) for v in out[:steps]]
+
+    def decode_forced(self, ids):
+        """Teacher-forced steps: step s feeds ids[s]; returns the greedy
+        argmax of the logits each step started from."""
+        import numpy as np
+        t = np.ascontiguousarray(ids, dtype=np.uint32)
+        out = np.zeros(max(t.size, 1), np.uint32)
+        _check(lib().myos_decode_forced(self._h, t.ctypes.data_as(P), t.size,
+                                        out.ctypes.data_as(P)), "decode_forced")
+        return [int(v) for v in out[:t.size]]
+
+    def debug_raise_wait_error(self):
+        """Test hook: the next persistent launch's waits give up at once."""
+        _check(lib().myos_debug_raise_wait_error(self._h), "debug_raise_wait_error")
 
     def cache_len(self) -> int:
         return int(lib().myos_cache_len(self._h))

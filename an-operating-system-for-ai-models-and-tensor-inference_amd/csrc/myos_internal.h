@@ -79,8 +79,11 @@ struct ArgmaxFinalArgs {
   const float2 *part = nullptr;
   int nparts = 0;
   uint32_t *token_out = nullptr;       // plain result
-  uint32_t *state = nullptr;           // [pos, token, step, mode]; mode 1 = take state[1]
+  // [pos, token, step, mode]; mode 0 = feed the argmax, 1 = feed state[1],
+  // 2 = feed force[step] (the argmax is still recorded in out_ids[step])
+  uint32_t *state = nullptr;
   uint32_t *out_ids = nullptr;
+  const uint32_t *force = nullptr;
   const uint16_t *embed = nullptr;
   float *x = nullptr;
   int hidden = 0;
@@ -146,8 +149,7 @@ hipError_t launch_permute_rows(uint16_t *dst, const uint16_t *src, const int *pe
 struct PersistLayer {
   const uint16_t *ln1, *wqkv, *wo, *ln2, *wgu, *wd;
   const float *bqkv;
-  const uint16_t *wdT;         // down transposed [I][H] (streamed kernel only)
-  // down as column pairs [I/2][H]: word (j, r) = (wd[r][2j], wd[r][2j+1]) (first kernel)
+  // down as column pairs [I/2][H]: word (j, r) = (wd[r][2j], wd[r][2j+1])
   const uint32_t *wdp;
 };
 struct PersistArgs {
@@ -160,9 +162,7 @@ struct PersistArgs {
   size_t layer_kv;
   // tagged exchange buffers (zeroed once; tags only grow)
   uint64_t *tq, *tkv, *tpart, *tatt, *txo, *txd, *targ;
-  uint64_t *tpd;               // streamed kernel: [grid][H] down partials per workgroup
-  uint64_t *tpr;               // first kernel: down partials, [owner][grid][rows per owner]
-  int ring_slots;              // streamed kernel: set by the launcher
+  uint64_t *tpr;               // down partials, [owner][grid][rows per owner]
   // outputs
   float *logits, *normed, *x_out;
   float2 *part_out;
@@ -170,10 +170,11 @@ struct PersistArgs {
   const float2 *part_in;       // argmax partials of the forward before the launch
   int nparts_in;
   uint32_t *state, *out_ids;
+  const uint32_t *force;       // non-null: step s feeds force[s] (out_ids[s] keeps the argmax)
   uint32_t *err;
   uint32_t tag_base, steps, pos0;
   int lds_wd;                  // set by the launcher: LDS offset (floats) of the down block
-  int kv_bf16;                 // the cache at kc / vc holds bf16 (first kernel only)
+  int kv_bf16;                 // the cache at kc / vc holds bf16
   uint64_t *trace;             // optional [grid][5 L + 3] phase timestamps of one step
   uint32_t trace_step;
 };
@@ -184,21 +185,9 @@ bool persist_supported(int H, int I, int qdim, int d, int gq);
 bool persist_device_ok(const PersistArgs &a);  // shape, LDS and the current device fit
 hipError_t launch_decode_persistent(const PersistArgs &a, hipStream_t s);
 
-// ---- streamed persistent decode (myos_stream.hip) -----------------------------
-// The same contract as launch_decode_persistent; every workgroup keeps its
-// weight rows streaming from HBM across the dependency chain. Needs
-// PersistLayer::wdT and PersistArgs::tpd.
-bool stream_supported(int H, int I, int V, int qdim, int d, int gq, int nkv, int max_seq,
-                      int qkv_rows);
-bool stream_device_ok(const PersistArgs &a);
-hipError_t launch_decode_stream(const PersistArgs &a, hipStream_t s);
-size_t stream_tpd_words(int H);  // words of the down-partial buffer
-size_t stream_part_words(int nq, int max_seq, int d);  // attention partial words
 // dst[c][r] = src[r][c] for a [rows, cols] matrix of 32-bit words
 hipError_t launch_transpose_u32(uint32_t *dst, const uint32_t *src, int rows, int cols,
                                 hipStream_t s);
-hipError_t launch_transpose_bf16(uint16_t *dst, const uint16_t *src, int rows, int cols,
-                                 hipStream_t s);
 
 const char *kernel_build_info();
 

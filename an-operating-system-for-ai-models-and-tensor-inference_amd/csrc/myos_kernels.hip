@@ -655,8 +655,8 @@ __global__ void __launch_bounds__(1024) argmax_final_kernel(ArgmaxFinalArgs a) {
   __shared__ uint32_t tok_s;
   float bv = -INFINITY;
   uint32_t bi = 0xffffffffu;
-  const bool forced = a.state && a.state[3] == 1u;
-  if (!forced) {
+  const uint32_t mode = a.state ? a.state[3] : 0u;
+  if (mode != 1u) {
     // 8 partials per thread per round, all loaded before any compare
     for (int i0 = threadIdx.x; i0 < a.nparts; i0 += blockDim.x * 8) {
       float2 p[8];
@@ -675,7 +675,13 @@ __global__ void __launch_bounds__(1024) argmax_final_kernel(ArgmaxFinalArgs a) {
     float2 b = block_best(bv, bi, sh);
     if (threadIdx.x == 0) {
       uint32_t idx = __float_as_uint(b.y);
-      tok_s = idx < a.vocab ? idx : 0u;  // no candidate (all NaN / -inf) -> 0
+      idx = idx < a.vocab ? idx : 0u;  // no candidate (all NaN / -inf) -> 0
+      // teacher forcing: record the argmax, feed the given id
+      if (mode == 2u) {
+        if (a.out_ids) a.out_ids[a.state[2]] = idx;
+        idx = a.force[a.state[2]];
+      }
+      tok_s = idx;
     }
   } else if (threadIdx.x == 0) {
     tok_s = a.state[1];
@@ -686,7 +692,7 @@ __global__ void __launch_bounds__(1024) argmax_final_kernel(ArgmaxFinalArgs a) {
     if (a.token_out) *a.token_out = tok;
     if (a.state) {
       a.state[1] = tok;
-      if (a.out_ids) a.out_ids[a.state[2]] = tok;
+      if (a.out_ids && mode != 2u) a.out_ids[a.state[2]] = tok;
       a.state[2] += 1u;
     }
   }
@@ -1071,23 +1077,8 @@ __global__ void permute_rows_kernel(uint16_t *dst, const uint16_t *src, const in
   for (int j = threadIdx.x; j < cols; j += blockDim.x) o[j] = s[j];
 }
 
-// dst[c][r] = src[r][c] for a [rows, cols] bf16 matrix, 32x32 tiles through
-// LDS (one-time layout change at load)
-__global__ void transpose_bf16_kernel(uint16_t *dst, const uint16_t *src, int rows, int cols) {
-  __shared__ uint16_t t[32][33];
-  const int c0 = blockIdx.x * 32, r0 = blockIdx.y * 32;
-  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;  // 256 threads: 8 rows a pass
-  for (int y = ty; y < 32; y += 8) {
-    const int r = r0 + y, c = c0 + tx;
-    if (r < rows && c < cols) t[y][tx] = src[(size_t)r * cols + c];
-  }
-  __syncthreads();
-  for (int y = ty; y < 32; y += 8) {
-    const int c = c0 + y, r = r0 + tx;
-    if (r < rows && c < cols) dst[(size_t)c * rows + r] = t[tx][y];
-  }
-}
-
+// dst[c][r] = src[r][c] for a [rows, cols] matrix of 32-bit words, 32x32 tiles
+// through LDS (one-time layout change at load)
 __global__ void transpose_u32_kernel(uint32_t *dst, const uint32_t *src, int rows, int cols) {
   __shared__ uint32_t t[32][33];
   const int c0 = blockIdx.x * 32, r0 = blockIdx.y * 32;
@@ -1550,14 +1541,6 @@ hipError_t launch_permute_rows(uint16_t *dst, const uint16_t *src, const int *pe
                                int cols, hipStream_t s) {
   if (rows <= 0) return hipSuccess;
   hipLaunchKernelGGL(permute_rows_kernel, dim3(rows), dim3(256), 0, s, dst, src, perm, cols);
-  return hipGetLastError();
-}
-
-hipError_t launch_transpose_bf16(uint16_t *dst, const uint16_t *src, int rows, int cols,
-                                 hipStream_t s) {
-  if (rows <= 0 || cols <= 0) return hipSuccess;
-  hipLaunchKernelGGL(transpose_bf16_kernel, dim3(nblk(cols, 32), nblk(rows, 32)), dim3(256), 0, s,
-                     dst, src, rows, cols);
   return hipGetLastError();
 }
 

@@ -74,6 +74,7 @@ struct myos_model {
   float2 *part = nullptr;
   int nparts = 0;
   uint32_t *state = nullptr, *out_ids = nullptr;
+  uint32_t *force_ids = nullptr;  // teacher-forced ids of myos_decode_forced
   uint32_t *host_state = nullptr;  // pinned [4]
   // prefill workspace, grown on demand
   uint8_t *pf = nullptr;
@@ -96,13 +97,14 @@ struct myos_model {
   size_t pbuf_bytes = 0;
   PersistLayer *dlayers = nullptr;
   PersistArgs pargs{};            // all but tag_base / steps / pos0
-  bool persist_stream = false;    // the streamed kernel (myos_stream.hip) runs it
-  uint16_t *wdT = nullptr;        // streamed kernel: down transposed, [L][I][H];
-                                  // first kernel: down as column pairs, [L][I/2][H] words
+  uint32_t *wdp = nullptr;        // down as column pairs, [L][I/2][H] words
   uint32_t tag_base = 1;          // tags below this value are spent
   uint32_t *err = nullptr;
   uint64_t *trace = nullptr;      // phase timestamps (myos_set_decode_trace)
   int64_t trace_step = -1;
+  // a persistent launch gave up on a wait: logits, argmax partials and the
+  // residual are garbage; decode calls are refused until prefill or cache_clear
+  bool poisoned = false;
 
   void *kc_layer(size_t l) const {
     return kc + l * layer_kv_elems * (kv_bf16 ? 2 : 4);
@@ -278,6 +280,7 @@ int enqueue_step(myos_model *m) {
   af.nparts = m->nparts;
   af.state = m->state;
   af.out_ids = m->out_ids;
+  af.force = m->force_ids;
   af.embed = m->embed;
   af.x = m->x;
   af.hidden = (int)m->s.hidden;
@@ -426,32 +429,21 @@ int setup_persistent(myos_model *m) {
   a.qkv_rows = (int)m->qkv_rows;
   a.eps = s.rms_eps;
   a.kv_bf16 = m->kv_bf16;
-  // MYOS_PERSIST_KERNEL=stream selects the streamed kernel (myos_stream.hip),
-  // which reads an f32 cache; a bf16 cache takes the first kernel
-  const char *pk = getenv("MYOS_PERSIST_KERNEL");
-  const bool want_stream = pk && std::string(pk) == "stream";
-  if (m->kv_bf16 && want_stream) return MYOS_OK;  // per-kernel path
-  a.tpd = nullptr;
   a.tpr = nullptr;
-  m->persist_stream = want_stream && stream_device_ok(a);
-  if (!m->persist_stream && !persist_device_ok(a)) return MYOS_OK;
-  const size_t words[9] = {m->q_dim, 2 * m->kv_dim,
-                           std::max(persist_part_words(a.nq, a.max_seq, a.d),
-                                    stream_part_words(a.nq, a.max_seq, a.d)),
+  if (!persist_device_ok(a)) return MYOS_OK;
+  const size_t words[8] = {m->q_dim, 2 * m->kv_dim, persist_part_words(a.nq, a.max_seq, a.d),
                            m->q_dim, s.hidden, s.hidden, 2 * (size_t)persist_grid(),
-                            m->persist_stream ? stream_tpd_words((int)s.hidden) : 0,
-                            m->persist_stream ? 0
-                                              : (size_t)persist_grid() * persist_grid() *
-                                                    ((s.hidden + persist_grid() - 1) / persist_grid())};
+                           (size_t)persist_grid() * persist_grid() *
+                               ((s.hidden + persist_grid() - 1) / persist_grid())};
   size_t total = 0;
   for (size_t w : words) total += align256(w * 8);
   total += 256;  // error word
   HIP_TRY(hipMalloc((void **)&m->pbuf, total));
   HIP_TRY(hipMemsetAsync(m->pbuf, 0, total, m->stream));
   m->pbuf_bytes = total;
-  uint64_t **dst[9] = {&a.tq, &a.tkv, &a.tpart, &a.tatt, &a.txo, &a.txd, &a.targ, &a.tpd, &a.tpr};
+  uint64_t **dst[8] = {&a.tq, &a.tkv, &a.tpart, &a.tatt, &a.txo, &a.txd, &a.targ, &a.tpr};
   uint8_t *p = m->pbuf;
-  for (int i = 0; i < 9; i++) {
+  for (int i = 0; i < 8; i++) {
     *dst[i] = (uint64_t *)p;
     p += align256(words[i] * 8);
   }
@@ -459,24 +451,15 @@ int setup_persistent(myos_model *m) {
   a.err = m->err;
   std::vector<PersistLayer> hl(s.num_layers);
   const size_t dsz = s.intermediate * s.hidden;  // elements of one down matrix
-  // both cooperative kernels read down by columns: the streamed one as a
-  // transposed copy, the first one as column pairs (one word per row of a pair)
-  HIP_TRY(hipMalloc((void **)&m->wdT, s.num_layers * dsz * 2));
-  for (size_t l = 0; l < s.num_layers; l++) {
-    if (m->persist_stream)
-      HIP_TRY(launch_transpose_bf16(m->wdT + l * dsz, m->layers[l].wd, (int)s.hidden,
-                                    (int)s.intermediate, m->stream));
-    else
-      HIP_TRY(launch_transpose_u32((uint32_t *)(m->wdT + l * dsz),
-                                   (const uint32_t *)m->layers[l].wd, (int)s.hidden,
-                                   (int)s.intermediate / 2, m->stream));
-  }
+  // the cooperative kernel reads down by columns: a copy of it as column
+  // pairs (one 32-bit word per row of a pair)
+  HIP_TRY(hipMalloc((void **)&m->wdp, s.num_layers * dsz * 2));
+  for (size_t l = 0; l < s.num_layers; l++)
+    HIP_TRY(launch_transpose_u32(m->wdp + l * dsz / 2, (const uint32_t *)m->layers[l].wd,
+                                 (int)s.hidden, (int)s.intermediate / 2, m->stream));
   for (size_t l = 0; l < s.num_layers; l++) {
     const DevLayer &L = m->layers[l];
-    uint16_t *t = m->wdT + l * dsz;
-    hl[l] = PersistLayer{L.ln1, L.wqkv, L.wo, L.ln2, L.wgu, L.wd, L.bqkv,
-                         m->persist_stream ? t : nullptr,
-                         m->persist_stream ? nullptr : (const uint32_t *)t};
+    hl[l] = PersistLayer{L.ln1, L.wqkv, L.wo, L.ln2, L.wgu, L.wd, L.bqkv, m->wdp + l * dsz / 2};
   }
   HIP_TRY(hipMalloc((void **)&m->dlayers, hl.size() * sizeof(PersistLayer)));
   HIP_TRY(hipMemcpy(m->dlayers, hl.data(), hl.size() * sizeof(PersistLayer),
@@ -498,6 +481,7 @@ int setup_persistent(myos_model *m) {
   a.nparts_in = m->nparts;
   a.state = m->state;
   a.out_ids = m->out_ids;
+  a.force = nullptr;
   m->persist_ok = true;
   return MYOS_OK;
 }
@@ -510,7 +494,7 @@ bool use_persistent(const myos_model *m) {
 
 // n greedy steps from the cursor in one cooperative launch; the error word
 // is checked after the stream synchronizes
-int persist_decode(myos_model *m, size_t n) {
+int persist_decode(myos_model *m, size_t n, bool forced = false) {
   const uint64_t tps = (uint64_t)persist_tags_per_step((int)m->s.num_layers);
   if ((uint64_t)m->tag_base + n * tps >= 0xffffffffull) {
     // the next tags would wrap: start again from zeroed words
@@ -521,12 +505,12 @@ int persist_decode(myos_model *m, size_t n) {
   a.tag_base = m->tag_base;
   a.steps = (uint32_t)n;
   a.pos0 = (uint32_t)m->len;
+  a.force = forced ? m->force_ids : nullptr;
   if (m->trace_step >= 0 && (size_t)m->trace_step < n) {
     a.trace = m->trace;
     a.trace_step = (uint32_t)m->trace_step;
   }
-  const hipError_t e = m->persist_stream ? launch_decode_stream(a, m->stream)
-                                         : launch_decode_persistent(a, m->stream);
+  const hipError_t e = launch_decode_persistent(a, m->stream);
   if (e == hipErrorCooperativeLaunchTooLarge || e == hipErrorInvalidConfiguration) {
     (void)hipGetLastError();
     return kLaunchRefused;  // nothing ran: the caller takes the per-kernel path
@@ -540,13 +524,47 @@ int persist_check_error(myos_model *m) {
   uint32_t e = 0;
   HIP_TRY(hipMemcpy(&e, m->err, 4, hipMemcpyDeviceToHost));
   if (e) {
-    // a wait timed out: the run's ids and cache rows are not trustworthy
+    // a wait timed out: the run's ids, logits and cache rows are not
+    // trustworthy, so nothing continues from them
     HIP_TRY(hipMemset(m->err, 0, 4));
+    m->poisoned = true;
     return MYOS_E_HIP;
   }
   return MYOS_OK;
 }
 
+// n decode steps from the cursor on the selected path: greedy (mode 0) or
+// fed from force_ids (mode 2); out receives the argmax of each step's input
+// logits; the cursor advances by n
+int decode_run(myos_model *m, size_t n, uint32_t mode, uint32_t *out) {
+  bool persist = use_persistent(m);
+  if (!persist) prepare_graph(m);  // capture (once) outside the timed region
+  int rc = write_state(m, (uint32_t)m->len, 0, 0, mode);
+  if (rc) return rc;
+  HIP_TRY(hipEventRecord(m->ev0, m->stream));
+  rc = persist ? persist_decode(m, n, mode == 2) : run_steps(m, n);
+  if (rc == kLaunchRefused) {
+    // the device cannot hold the cooperative grid: per-kernel path from now on
+    m->persist_ok = false;
+    persist = false;
+    prepare_graph(m);
+    HIP_TRY(hipEventRecord(m->ev0, m->stream));
+    rc = run_steps(m, n);
+  }
+  if (rc) return rc;
+  HIP_TRY(hipEventRecord(m->ev1, m->stream));
+  HIP_TRY(hipStreamSynchronize(m->stream));
+  if (persist) {
+    rc = persist_check_error(m);
+    if (rc) return rc;
+  }
+  HIP_TRY(hipMemcpy(out, m->out_ids, n * 4, hipMemcpyDeviceToHost));
+  float ms = 0;
+  HIP_TRY(hipEventElapsedTime(&ms, m->ev0, m->ev1));
+  m->decode_ms = ms;
+  m->len += n;
+  return MYOS_OK;
+}
 }  // namespace
 
 extern "C" {
@@ -594,7 +612,7 @@ void myos_model_close(myos_model *m) {
   if (m->pf) (void)hipFree(m->pf);
   if (m->pbuf) (void)hipFree(m->pbuf);
   if (m->dlayers) (void)hipFree(m->dlayers);
-  if (m->wdT) (void)hipFree(m->wdT);
+  if (m->wdp) (void)hipFree(m->wdp);
   if (m->trace) (void)hipFree(m->trace);
   if (m->host_state) (void)hipHostFree(m->host_state);
   if (m->stream) (void)hipStreamDestroy(m->stream);
@@ -781,7 +799,7 @@ static int open_impl(myos_model *m, const char *path, const myos_block_shape *sh
       align256(attn_decode_part_floats((int)s.num_q_heads, (int)max_seq, (int)s.head_dim) * 4);
   const size_t b_st = align256(16);
   const size_t b_ids = align256(max_seq * 4);
-  m->ws_bytes = 2 * b_x + 2 * b_q + b_h + b_lg + b_part + b_ap + b_st + b_ids;
+  m->ws_bytes = 2 * b_x + 2 * b_q + b_h + b_lg + b_part + b_ap + b_st + 2 * b_ids;
   HIP_TRY(hipMalloc((void **)&m->ws, m->ws_bytes));
   HIP_TRY(hipMemsetAsync(m->ws, 0, m->ws_bytes, m->stream));
   p = m->ws;
@@ -804,6 +822,8 @@ static int open_impl(myos_model *m, const char *path, const myos_block_shape *sh
   m->state = (uint32_t *)p;
   p += b_st;
   m->out_ids = (uint32_t *)p;
+  p += b_ids;
+  m->force_ids = (uint32_t *)p;
   // argmax of the all-zero logits BlockWorkspace starts with is id 0
   std::vector<float2> part0(m->nparts);
   uint32_t none = 0xffffffffu, zero = 0;
@@ -955,12 +975,14 @@ int myos_prefill(myos_model *m, const uint32_t *tokens, size_t n) {
   HIP_TRY(hipEventElapsedTime(&ms, m->ev0, m->ev1));
   m->prefill_ms = ms;
   m->len = end;
+  m->poisoned = false;  // logits, argmax partials and residual are fresh again
   return MYOS_OK;
 }
 
 // qwen25_block.rs:220-304
 int myos_forward_token(myos_model *m, uint32_t token, size_t pos) {
   if (!m) return MYOS_E_ARG;
+  if (m->poisoned) return MYOS_E_HIP;
   if (pos != m->len) return MYOS_E_POSITION;
   if (pos >= m->max_seq) return MYOS_E_KV_FULL;
   if ((size_t)token >= m->s.vocab) return MYOS_E_TOKEN;
@@ -976,37 +998,26 @@ int myos_forward_token(myos_model *m, uint32_t token, size_t pos) {
 // qwen25_block.rs:765-780
 int myos_greedy_decode(myos_model *m, size_t steps, uint32_t *out) {
   if (!m || (!out && steps)) return MYOS_E_ARG;
+  if (m->poisoned) return MYOS_E_HIP;
   const size_t room = m->max_seq - m->len;
   const size_t n = steps < room ? steps : room;
   if (n) {
-    bool persist = use_persistent(m);
-    if (!persist) prepare_graph(m);  // capture (once) outside the timed region
-    int rc = write_state(m, (uint32_t)m->len, 0, 0, 0);
+    int rc = decode_run(m, n, 0, out);
     if (rc) return rc;
-    HIP_TRY(hipEventRecord(m->ev0, m->stream));
-    rc = persist ? persist_decode(m, n) : run_steps(m, n);
-    if (rc == kLaunchRefused) {
-      // the device cannot hold the cooperative grid: per-kernel path from now on
-      m->persist_ok = false;
-      persist = false;
-      prepare_graph(m);
-      HIP_TRY(hipEventRecord(m->ev0, m->stream));
-      rc = run_steps(m, n);
-    }
-    if (rc) return rc;
-    HIP_TRY(hipEventRecord(m->ev1, m->stream));
-    HIP_TRY(hipStreamSynchronize(m->stream));
-    if (persist) {
-      rc = persist_check_error(m);
-      if (rc) return rc;
-    }
-    HIP_TRY(hipMemcpy(out, m->out_ids, n * 4, hipMemcpyDeviceToHost));
-    float ms = 0;
-    HIP_TRY(hipEventElapsedTime(&ms, m->ev0, m->ev1));
-    m->decode_ms = ms;
-    m->len += n;
   }
   return n < steps ? MYOS_E_KV_FULL : MYOS_OK;
+}
+
+int myos_decode_forced(myos_model *m, const uint32_t *ids, size_t steps, uint32_t *argmax_out) {
+  if (!m || (steps && (!ids || !argmax_out))) return MYOS_E_ARG;
+  if (m->poisoned) return MYOS_E_HIP;
+  if (steps > m->max_seq - m->len) return MYOS_E_KV_FULL;
+  for (size_t i = 0; i < steps; i++)
+    if ((size_t)ids[i] >= m->s.vocab) return MYOS_E_TOKEN;
+  if (!steps) return MYOS_OK;
+  HIP_TRY(hipStreamSynchronize(m->stream));
+  HIP_TRY(hipMemcpy(m->force_ids, ids, steps * 4, hipMemcpyHostToDevice));
+  return decode_run(m, steps, 2, argmax_out);
 }
 
 size_t myos_cache_len(const myos_model *m) { return m ? m->len : 0; }
@@ -1014,6 +1025,7 @@ size_t myos_cache_len(const myos_model *m) { return m ? m->len : 0; }
 int myos_cache_clear(myos_model *m) {
   if (!m) return MYOS_E_ARG;
   m->len = 0;
+  m->poisoned = false;
   return write_state(m, 0, 0, 0, 0);
 }
 
@@ -1142,6 +1154,15 @@ int myos_set_decode_trace(myos_model *m, int64_t step) {
     HIP_TRY(hipMemset(m->trace, 0, n * sizeof(uint64_t)));
   }
   m->trace_step = step;
+  return MYOS_OK;
+}
+
+int myos_debug_raise_wait_error(myos_model *m) {
+  if (!m) return MYOS_E_ARG;
+  if (!m->persist_ok) return MYOS_E_SHAPE;
+  const uint32_t one = 1;
+  HIP_TRY(hipMemcpyAsync(m->err, &one, 4, hipMemcpyHostToDevice, m->stream));
+  HIP_TRY(hipStreamSynchronize(m->stream));
   return MYOS_OK;
 }
 

@@ -659,8 +659,10 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
           if (beats(best_s[w].x, __float_as_uint(best_s[w].y), b.x, __float_as_uint(b.y)))
             b = best_s[w];
         const uint32_t idx = __float_as_uint(b.y);
-        tok_s = idx < (uint32_t)V ? idx : 0u;  // no candidate (all NaN / -inf) -> 0
-        if (wg == 0) a.out_ids[s] = tok_s;
+        const uint32_t best = idx < (uint32_t)V ? idx : 0u;  // no candidate (all NaN / -inf) -> 0
+        if (wg == 0) a.out_ids[s] = best;
+        tok_s = a.force ? a.force[s] : best;  // teacher forcing feeds the given id
+        if (wg == 0 && s + 1 == a.steps) a.state[1] = tok_s;
       }
       __syncthreads();
       const uint16_t *erow = a.embed + (size_t)tok_s * H;
@@ -1154,7 +1156,6 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
           b = best_s[w];
       best_s[0] = b;
       a.state[0] = a.pos0 + a.steps;
-      a.state[1] = a.out_ids[a.steps - 1];
       a.state[2] = a.steps;
     }
     __syncthreads();

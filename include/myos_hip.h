@@ -145,7 +145,9 @@ int myos_model_open(const char *path, const myos_block_shape *shape, int kv_dtyp
 void myos_model_close(myos_model *m);
 
 /* prefill, qwen25_block.rs:323-543: the prompt as one chunk (MFMA GEMMs),
- * causal attention, logits for the last id, cursor += n. */
+ * causal attention, logits for the last id, cursor += n. A device error in a
+ * persistent decode launch leaves the model refusing decode calls until the
+ * next prefill or cache_clear (see myos_debug_raise_wait_error). */
 int myos_prefill(myos_model *m, const uint32_t *tokens, size_t n);
 /* forward_token, qwen25_block.rs:220-304. pos must equal the cursor. */
 int myos_forward_token(myos_model *m, uint32_t token, size_t pos);
@@ -154,6 +156,16 @@ int myos_forward_token(myos_model *m, uint32_t token, size_t pos);
  * MYOS_E_KV_FULL after the steps that fit, like the reference's loop. Each
  * step is one hipGraph replay when graphs are enabled (the default). */
 int myos_greedy_decode(myos_model *m, size_t steps, uint32_t *out);
+
+/* Teacher-forced decode (no reference counterpart: the reference's runtime
+ * compares free-running ids only, main.rs:672-686): `steps` steps from the
+ * cursor, step s feeding ids[s] as forward_token(ids[s], cursor) would, on the
+ * same path greedy_decode takes (one cooperative launch when persistent).
+ * argmax_out[s] receives greedy_token of the logits step s started from, so
+ * a caller can compare each step's greedy choice with a reference run fed the
+ * same ids. Checks before any launch: ids[s] >= vocab -> TOKEN; steps past
+ * max_seq -> KV_FULL (nothing runs). */
+int myos_decode_forced(myos_model *m, const uint32_t *ids, size_t steps, uint32_t *argmax_out);
 
 size_t myos_cache_len(const myos_model *m);        /* KvCache::len */
 /* KvCache::clear (kv_cache.rs:234-237): cursor back to 0, slots kept. */
@@ -173,9 +185,10 @@ int myos_set_graph(myos_model *m, int enabled);
  * has one CPU path). PERSISTENT runs the whole call as one cooperative kernel
  * whose workgroups hand activations to each other through tagged words;
  * KERNELS replays per-step graphs of per-layer kernels; AUTO (default) takes
- * PERSISTENT when the model allows it (f32 cache, hidden and q_dim <= 1536,
- * intermediate <= 9216, head_dim <= 128 and a multiple of 8) and the device has
- * >= 256 CUs with cooperative launch. Setting PERSISTENT where it is not
+ * PERSISTENT when the model allows it (f32 or bf16 cache, hidden and q_dim <=
+ * 1536 and multiples of 32 and 8, intermediate <= 9216, head_dim 32, 64 or
+ * 128, at most 8 q heads per kv head, and the kernel's LDS budget) and the
+ * device has >= 256 CUs with cooperative launch. Setting PERSISTENT where it is not
  * available returns MYOS_E_SHAPE. myos_decode_path returns the path the next
  * call takes. */
 enum { MYOS_DECODE_AUTO = 0, MYOS_DECODE_KERNELS = 1, MYOS_DECODE_PERSISTENT = 2 };
@@ -190,6 +203,12 @@ int myos_decode_path(const myos_model *m);
  * it off. myos_copy_decode_trace copies [grid][5 layers + 3] values, where
  * grid is 256; n must equal that count. MYOS_E_SHAPE without the path. */
 int myos_set_decode_trace(myos_model *m, int64_t step);
+/* Test hook for the persistent path's error handling (no reference
+ * counterpart): raises the kernel's error word, so every bounded wait of the
+ * next launch gives up at once and the launch returns MYOS_E_HIP. After such
+ * an error the model refuses forward_token / greedy_decode / decode_forced
+ * (MYOS_E_HIP) until a prefill or cache_clear. MYOS_E_SHAPE without the path. */
+int myos_debug_raise_wait_error(myos_model *m);
 int myos_copy_decode_trace(const myos_model *m, uint64_t *out, size_t n);
 /* Device time of the last prefill / greedy_decode (hipEvent, milliseconds). */
 double myos_last_prefill_ms(const myos_model *m);

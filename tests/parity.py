@@ -43,6 +43,35 @@ def top2_gap(logits):
     return float(v[i] - rest.max()) if rest.size else float("inf")
 
 
+def check_step_id(got_id, ref_logits, what="", gap=GAP):
+    """One decode step's id under the tolerance rule: where the oracle's
+    top-1 / top-2 gap exceeds `gap` the id must be the oracle's argmax; below
+    it, the id must be one of the near-tied candidates (its oracle logit
+    within `gap` of the top). Returns True when the id is the oracle's own."""
+    v = np.asarray(ref_logits, np.float64)
+    top = int(np.argmax(v))
+    if got_id == top:
+        return True
+    g = top2_gap(v)
+    assert g <= gap, f"{what}: id {got_id} != oracle {top} at top-2 gap {g:.3e}"
+    assert v[top] - v[got_id] <= gap, (
+        f"{what}: id {got_id} is {v[top] - v[got_id]:.3e} below the oracle's top {top}")
+    return False
+
+
+def follow_ids(o, ids, what="", gap=GAP):
+    """Let the oracle follow the GPU's generated ids: each id is checked
+    against the oracle's logits of that step (check_step_id) and then fed to
+    the oracle, so both stay on one trajectory through near-ties and the
+    states after the run are comparable. Returns the number of steps whose
+    id was the oracle's own argmax."""
+    exact = 0
+    for i, tok in enumerate(ids):
+        exact += check_step_id(int(tok), o.logits(), f"{what} step {i}", gap)
+        assert o.forward_token(int(tok), o.cache_len()) == 0
+    return exact
+
+
 def assert_logits_parity(got, ref, what=""):
     r = max_rel(got, ref)
     assert r <= REL_TOL, f"{what}: logits max rel err {r:.3e} > {REL_TOL}"

@@ -10,7 +10,6 @@
   teacher-forced decode, under the tolerance rule in parity.py.
 """
 import importlib
-import os
 
 import numpy as np
 import pytest
@@ -18,7 +17,7 @@ import pytest
 import oracle
 from model_fixtures import (block_fixture, random_map, rich_map, rich_shape, shape_dict,
                             write_safetensors)
-from parity import assert_logits_parity, max_rel, top2_gap
+from parity import assert_logits_parity, follow_ids, max_rel, top2_gap
 
 myos = importlib.import_module("an-operating-system-for-ai-models-and-tensor-inference_amd")
 pytestmark = pytest.mark.gpu
@@ -60,6 +59,108 @@ def test_block_fixture(tmp_path):
     assert g2.greedy_decode(4) == [1, 1, 1, 1] and g2.cache_len() == 5
     for gm in (g, g2):
         gm.close()
+
+
+def _both_paths(tmp_path, s, t, name, max_seq=4, tied=True):
+    """The model on both forward paths: the per-kernel forward_token and the
+    MFMA prefill."""
+    path = str(tmp_path / name)
+    write_safetensors(path, t)
+    a = myos.Model.open(path, to_block_shape(s, tied), myos.KV_F32, max_seq)
+    b = myos.Model.open(path, to_block_shape(s, tied), myos.KV_F32, max_seq)
+    return a, b
+
+
+def test_swiglu_residual_fixture(tmp_path, orc):
+    # qwen25_block.rs:1074-1129, the only reference block vector with a
+    # non-zero MLP: exact bits (every operand is small and exact), as pinned
+    # on the oracle
+    from model_fixtures import swiglu_residual_fixture
+    s, t = swiglu_residual_fixture()
+    o = orc.Model(s, t, 2, threads=1)
+    assert o.forward_token(0, 0) == 0
+    a, b = _both_paths(tmp_path, s, t, "swiglu.safetensors", 2)
+    a.forward_token(0, 0)
+    b.prefill([0])
+    # (the MFMA prefill carries h = silu(1) in 16 significant bits: 1e-4)
+    for m in (a, b):
+        assert max_rel(m.logits(), o.logits()) < 1e-4
+        assert max_rel(m.hidden(), o.hidden()) < 1e-4
+        assert m.cache_len() == 1 and list(m.kv(0, 0, 0)[1]) == [1.0, 0.0]
+        m.close()
+
+
+def test_two_layer_fixture(tmp_path, orc):
+    # qwen25_block.rs:1132-1197: per-layer V slots at one cursor, one advance
+    # per token, on the forward_token, prefill and persistent paths
+    from model_fixtures import two_layer_fixture
+    s, t = two_layer_fixture()
+    a, b = _both_paths(tmp_path, s, t, "two.safetensors", 4)
+    a.forward_token(0, 0)
+    b.prefill([0])
+    for m in (a, b):
+        assert list(m.logits()) == [1.0, 2.0, 0.0, -1.0] and m.cache_len() == 1
+        assert list(m.kv(0, 0, 0)[1]) == [2.0, 0.0] and list(m.kv(1, 0, 0)[1]) == [0.0, 8.0]
+        assert list(m.kv(0, 0, 1)[1]) == [0.0, 0.0] and list(m.kv(1, 0, 1)[1]) == [0.0, 0.0]
+    a.forward_token(1, 1)
+    b.decode_forced([1])
+    o = orc.Model(s, t, 4, threads=1)
+    assert o.forward_token(0, 0) == 0 and o.forward_token(1, 1) == 0
+    for m in (a, b):
+        assert m.cache_len() == 2
+        assert list(m.kv(0, 0, 1)[1]) == [2.0, 0.0] and list(m.kv(1, 0, 1)[1]) == [0.0, 8.0]
+        assert max_rel(m.logits(), o.logits()) < 1e-4
+        assert int(np.argmax(m.logits())) == 1
+        m.close()
+
+
+def test_post_attention_norm_fixture(tmp_path, orc):
+    # the closed-form fixture whose ln2 differs from ln1 (see the oracle pin
+    # test_post_attention_norm_feeds_the_mlp)
+    from model_fixtures import (bits, block_fixture_layer, fixture_embed_and_final,
+                                fixture_shape)
+    s = fixture_shape()
+    t = fixture_embed_and_final((1.0, 0.5))
+    block_fixture_layer(t, 0, [0.0] * 4, [1.0, 0.0], [1.0, 0.0, 0.0, 0.0, 1.0, 0.0, 0.0, 0.0],
+                        [1.0, 0.0, 0.0, 0.0], [1.0, 0.0, 0.0, 1.0], [1.0, 0.0, 0.5, 0.0])
+    t["model.layers.0.post_attention_layernorm.weight"] = bits([2.0, 0.0])
+    o = orc.Model(s, t, 2, threads=1)
+    assert o.forward_token(0, 0) == 0
+    a, b = _both_paths(tmp_path, s, t, "norm2.safetensors", 2)
+    a.forward_token(0, 0)
+    b.prefill([0])
+    for m in (a, b):
+        assert max_rel(m.hidden(), o.hidden()) < 1e-4
+        assert max_rel(m.logits(), o.logits()) < 1e-4
+        m.close()
+
+
+def test_untied_head_copy_equals_tied(tmp_path, orc):
+    # an lm_head.weight equal to the embedding gives the tied head's logits;
+    # a different one moves only the logits, and both match the oracle
+    s = shape_dict(256, 4, 2, 64, 512, 1000, 2, 1e-6)
+    t = random_map(s, seed=21, std=0.05)
+    tu = dict(t)
+    tu["lm_head.weight"] = np.array(t["model.embed_tokens.weight"], copy=True)
+    td = dict(t)
+    td["lm_head.weight"] = random_map(s, seed=22, std=0.05)["model.embed_tokens.weight"]
+    prompt = [7, 300, 41, 999, 5]
+    res = {}
+    for name, tens, tied in (("tied", t, True), ("copy", tu, False), ("other", td, False)):
+        path = str(tmp_path / f"{name}.safetensors")
+        write_safetensors(path, tens)
+        g = myos.Model.open(path, to_block_shape(s, tied), myos.KV_F32, 16)
+        g.prefill(prompt)
+        ids = g.greedy_decode(6)
+        res[name] = (g.logits(), g.hidden(), ids)
+        o = orc.Model(s, tens, 16, threads=2)
+        assert o.prefill(prompt) == 0
+        follow_ids(o, ids, name)
+        assert_logits_parity(g.logits(), o.logits(), name)
+        assert max_rel(g.logits(), o.logits()) < 1e-4
+        g.close()
+    assert np.array_equal(res["copy"][0], res["tied"][0]) and res["copy"][2] == res["tied"][2]
+    assert not np.array_equal(res["other"][0], res["tied"][0])
 
 
 def test_errors_do_not_advance(tmp_path):
@@ -178,13 +279,9 @@ def test_prefill_attention_key_groups(tmp_path, dims, m):
 # -------------------------------------------------- Qwen2.5-1.5B shape ----
 
 @pytest.fixture(scope="module")
-def qwen15(tmp_path_factory):
-    path = os.environ.get("MYOS_TEST_WEIGHTS_1_5B")
-    if not path:
-        path = str(tmp_path_factory.mktemp("w") / "qwen25_1_5b_seed0.safetensors")
-        myos.write_random_qwen25(path, myos.preset(myos.SHAPE_QWEN25_1_5B), seed=0, std=0.02)
+def qwen15(qwen15_path):
     s = shape_dict(1536, 12, 2, 128, 8960, 151936, 28, 1e-6)
-    return path, s, oracle.load_safetensors_bits(path)
+    return qwen15_path, s, oracle.load_safetensors_bits(qwen15_path)
 
 
 def test_qwen15_prompt0_four_steps(qwen15):

@@ -4,64 +4,53 @@ against the oracle and against the per-kernel path.
 The persistent kernel computes the same step as forward_token
 (qwen25_block.rs:220-304) inside greedy_decode (qwen25_block.rs:765-780), with
 its own summation order, so it is held to the same rule as the per-kernel
-path: logits / hidden within max relative error 1e-2 and ids equal at every
-step where the oracle's top-1 / top-2 gap exceeds 1e-3 (after an allowed
-divergence at a smaller gap the trajectories separate and comparison stops).
-It also has to leave the decode state (cursor, cache rows, logits, argmax of
-the last logits) exactly where the per-kernel path expects it.
+path: every generated id must be the oracle's greedy id wherever the oracle's
+top-1 / top-2 gap exceeds 1e-3 (one of the near-tied ids below it), and
+logits / hidden state within max relative error 1e-2. The oracle follows the
+GPU's ids (parity.follow_ids): each GPU id is checked against the oracle's
+logits of that step and then fed to the oracle, so the two stay on one
+trajectory and the state after every run -- cursor, cache rows, logits,
+hidden -- is always compared, never skipped.
 """
 import importlib
-import os
 
 import numpy as np
 import pytest
 
 import oracle
 from model_fixtures import random_map, shape_dict, write_safetensors
-from parity import GAP, assert_logits_parity, max_rel, top2_gap
+from parity import GAP, assert_logits_parity, check_step_id, follow_ids, max_rel
 
 myos = importlib.import_module("an-operating-system-for-ai-models-and-tensor-inference_amd")
 pytestmark = pytest.mark.gpu
 
+# a bf16 KV cache (rounded to nearest even) moves logits by up to ~1e-2
+# relative against the f32-cache oracle: near-ties are then taken at 5e-2
+BF16_GAP = 5e-2
 
-def to_block_shape(s):
+
+def to_block_shape(s, tied=True):
     return myos.make_shape(s["hidden"], s["num_q_heads"], s["num_kv_heads"], s["head_dim"],
                            s["intermediate"], s["vocab"], s["num_layers"],
                            rms_eps=float(s["rms_eps"]), rope_theta=float(s["rope_theta"]),
-                           tied_head=True)
+                           tied_head=tied)
 
 
-def oracle_steps(o, n):
-    """Greedy steps on the oracle, keeping each step's top-1 / top-2 gap."""
-    ids, gaps = [], []
-    for _ in range(n):
-        lg = o.logits()
-        tok = oracle.greedy_token(lg)
-        ids.append(int(tok))
-        gaps.append(top2_gap(lg))
-        assert o.forward_token(tok, o.cache_len()) == 0
-    return ids, gaps
+def open_persistent(path, s, kv, max_seq):
+    g = myos.Model.open(path, to_block_shape(s), kv, max_seq)
+    if g.decode_path() != myos.DECODE_PERSISTENT:
+        g.close()
+        pytest.skip("the device cannot hold the cooperative decode grid")
+    return g
 
 
-def agree(got, ref, gaps):
-    """Index of the first allowed divergence (len if none); fails on a real one."""
-    for i, (a, b) in enumerate(zip(got, ref)):
-        if a != b:
-            assert gaps[i] <= GAP, f"id {i}: {a} != {b} at top-2 gap {gaps[i]:.3e}"
-            return i
-    return len(ref)
-
-
-@pytest.fixture(params=["first", "stream"], autouse=True)
-def persist_kernel(request, monkeypatch):
-    """Every test runs with each cooperative decode kernel: the first
-    (myos_persistent.hip, the default) and the streamed one
-    (myos_stream.hip, MYOS_PERSIST_KERNEL=stream), chosen at model open."""
-    if request.param == "stream":
-        monkeypatch.setenv("MYOS_PERSIST_KERNEL", "stream")
-    else:
-        monkeypatch.delenv("MYOS_PERSIST_KERNEL", raising=False)
-    return request.param
+def check_kv(g, o, s, positions, tol, heads=None):
+    for layer in range(s["num_layers"]):
+        for h in heads if heads is not None else range(s["num_kv_heads"]):
+            for pos in positions:
+                kg, vg = g.kv(layer, h, pos)
+                ko, vo = o.kv(layer, h, pos)
+                assert max_rel(kg, ko) < tol and max_rel(vg, vo) < tol, (layer, h, pos)
 
 
 SMALL = [(256, 4, 2, 64, 512, 1000, 3), (128, 6, 1, 32, 384, 777, 2),
@@ -75,10 +64,7 @@ def test_persistent_small_models(tmp_path, dims):
     path = str(tmp_path / "m.safetensors")
     write_safetensors(path, t)
     max_seq = 80
-    g = myos.Model.open(path, to_block_shape(s), myos.KV_F32, max_seq)
-    if g.decode_path() != myos.DECODE_PERSISTENT:
-        g.close()
-        pytest.skip("the device cannot hold the cooperative decode grid")
+    g = open_persistent(path, s, myos.KV_F32, max_seq)
     k = myos.Model.open(path, to_block_shape(s), myos.KV_F32, max_seq)
     k.set_decode_mode(myos.DECODE_KERNELS)
     assert k.decode_path() == myos.DECODE_KERNELS
@@ -89,49 +75,79 @@ def test_persistent_small_models(tmp_path, dims):
     assert o.prefill(prompt) == 0
     # two launches: the second starts from the state the first left behind
     ids_g = g.greedy_decode(20) + g.greedy_decode(23)
-    ids_k = k.greedy_decode(20) + k.greedy_decode(23)
-    ids_o, gaps = oracle_steps(o, 43)
-    n_ok = min(agree(ids_g, ids_o, gaps), agree(ids_k, ids_o, gaps))
-    assert g.cache_len() == k.cache_len() == 60
-    if n_ok == 43:
-        assert_logits_parity(g.logits(), o.logits(), "persistent, after 43 steps")
-        assert max_rel(g.hidden(), o.hidden()) < 1e-4
-        assert max_rel(g.normed(), o.normed()) < 1e-4
-        assert max_rel(g.logits(), k.logits()) < 1e-4
-        for layer in range(s["num_layers"]):
-            for pos in (0, 16, 17, 40, 59):
-                kg, vg = g.kv(layer, s["num_kv_heads"] - 1, pos)
-                ko, vo = o.kv(layer, s["num_kv_heads"] - 1, pos)
-                assert max_rel(kg, ko) < 1e-4 and max_rel(vg, vo) < 1e-4, (layer, pos)
-        # the per-kernel path continues from the persistent state
-        tok = oracle.greedy_token(o.logits())
-        g.forward_token(tok, 60)
-        assert o.forward_token(tok, 60) == 0
-        assert_logits_parity(g.logits(), o.logits(), "forward_token after persistent")
-        # ... and the persistent path from the per-kernel state
-        ids_o2, gaps2 = oracle_steps(o, 5)
-        agree(g.greedy_decode(5), ids_o2, gaps2)
+    follow_ids(o, ids_g, "persistent")
+    # the per-kernel path, fed the same ids, must agree with both
+    k.decode_forced(ids_g)
+    assert g.cache_len() == k.cache_len() == o.cache_len() == 60
+    assert_logits_parity(g.logits(), o.logits(), "persistent, after 43 steps")
+    assert max_rel(g.hidden(), o.hidden()) < 1e-4
+    assert max_rel(g.normed(), o.normed()) < 1e-4
+    assert max_rel(g.logits(), k.logits()) < 1e-4
+    check_kv(g, o, s, (0, 16, 17, 40, 59), 1e-4, heads=[s["num_kv_heads"] - 1])
+    # the per-kernel path continues from the persistent state
+    tok = oracle.greedy_token(o.logits())
+    g.forward_token(tok, 60)
+    assert o.forward_token(tok, 60) == 0
+    assert_logits_parity(g.logits(), o.logits(), "forward_token after persistent")
+    # ... and the persistent path from the per-kernel state
+    follow_ids(o, g.greedy_decode(5), "persistent after forward_token")
+    assert_logits_parity(g.logits(), o.logits(), "persistent after forward_token")
     g.close()
     k.close()
 
 
 @pytest.mark.parametrize("dims", SMALL[:2] + SMALL[3:])
-def test_persistent_bf16_cache(tmp_path, dims, persist_kernel):
-    """A bf16 KV cache: the first cooperative kernel stores and reads bf16
-    rows (rounded to nearest even, as the per-kernel path stores them). Both
-    paths against the f32-cache oracle: the cache rounding moves logits by up
-    to ~1e-2 relative, so ids must agree wherever the oracle's top-2 gap is
-    above 5e-2, and the two paths must agree with each other as closely."""
-    if persist_kernel == "stream":
-        pytest.skip("the streamed kernel reads an f32 cache: a bf16 cache takes the per-kernel path")
+def test_persistent_forced_small_models(tmp_path, dims):
+    """decode_forced on the cooperative kernel: each step feeds the given id
+    and reports the greedy id of the logits it started from; checked step by
+    step against the oracle fed the same ids, and the per-kernel path."""
+    s = shape_dict(*dims, 1e-6)
+    t = random_map(s, seed=sum(dims) + 2, std=0.05)
+    path = str(tmp_path / "m.safetensors")
+    write_safetensors(path, t)
+    g = open_persistent(path, s, myos.KV_F32, 64)
+    k = myos.Model.open(path, to_block_shape(s), myos.KV_F32, 64)
+    k.set_decode_mode(myos.DECODE_KERNELS)
+    o = oracle.Model(s, t, 64, threads=4)
+    prompt = np.random.default_rng(17).integers(0, s["vocab"], 9)
+    for m in (g, k):
+        m.prefill(prompt)
+    assert o.prefill(prompt) == 0
+    # forced ids that are NOT the greedy ones, so forcing is visible
+    forced = [int(v) for v in np.random.default_rng(19).integers(0, s["vocab"], 30)]
+    am_g = g.decode_forced(forced)
+    am_k = k.decode_forced(forced)
+    for i, tok in enumerate(forced):
+        check_step_id(am_g[i], o.logits(), f"persistent forced step {i}")
+        check_step_id(am_k[i], o.logits(), f"per-kernel forced step {i}")
+        assert o.forward_token(tok, o.cache_len()) == 0
+    assert g.cache_len() == k.cache_len() == o.cache_len() == 39
+    assert_logits_parity(g.logits(), o.logits(), "persistent forced")
+    assert max_rel(g.logits(), o.logits()) < 1e-4
+    assert max_rel(k.logits(), o.logits()) < 1e-4
+    check_kv(g, o, s, (0, 8, 9, 38), 1e-4)
+    # forced ids are validated before anything runs
+    with pytest.raises(myos.MyosError) as e:
+        g.decode_forced([0, s["vocab"]])
+    assert e.value.kind == "TokenOutOfBounds" and g.cache_len() == 39
+    with pytest.raises(myos.MyosError) as e:
+        g.decode_forced([0] * 26)
+    assert e.value.kind == "Full" and g.cache_len() == 39
+    g.close()
+    k.close()
+
+
+@pytest.mark.parametrize("dims", SMALL[:2] + SMALL[3:])
+def test_persistent_bf16_cache(tmp_path, dims):
+    """A bf16 KV cache: the cooperative kernel stores and reads bf16 rows
+    (rounded to nearest even, as the per-kernel path stores them). Against
+    the f32-cache oracle, ids follow at BF16_GAP and logits within 2e-2; the
+    per-kernel path fed the same ids must agree with it closely."""
     s = shape_dict(*dims, 1e-6)
     t = random_map(s, seed=sum(dims) + 3, std=0.05)
     path = str(tmp_path / "m.safetensors")
     write_safetensors(path, t)
-    g = myos.Model.open(path, to_block_shape(s), myos.KV_BF16, 80)
-    if g.decode_path() != myos.DECODE_PERSISTENT:
-        g.close()
-        pytest.skip("the device cannot hold the cooperative decode grid")
+    g = open_persistent(path, s, myos.KV_BF16, 80)
     k = myos.Model.open(path, to_block_shape(s), myos.KV_BF16, 80)
     k.set_decode_mode(myos.DECODE_KERNELS)
     o = oracle.Model(s, t, 80, threads=4)
@@ -139,51 +155,43 @@ def test_persistent_bf16_cache(tmp_path, dims, persist_kernel):
     for m in (g, k):
         m.prefill(prompt)
     assert o.prefill(prompt) == 0
-    ids_g, ids_k = g.greedy_decode(30), k.greedy_decode(30)
-    ids_o, gaps = oracle_steps(o, 30)
-    for i in range(30):
-        if ids_g[i] != ids_o[i] or ids_k[i] != ids_o[i]:
-            assert gaps[i] <= 5e-2, f"id {i}: {ids_g[i]} / {ids_k[i]} != {ids_o[i]} at gap {gaps[i]:.3e}"
-            break
-    if ids_g == ids_k:
-        assert max_rel(g.logits(), k.logits()) < 2e-2
-        for layer in range(s["num_layers"]):
-            for pos in (0, 16, 17, 40):
-                kg, vg = g.kv(layer, 0, pos)
-                kk, vk = k.kv(layer, 0, pos)
-                assert max_rel(kg, kk) < 2e-2 and max_rel(vg, vk) < 2e-2, (layer, pos)
+    ids_g = g.greedy_decode(30)
+    follow_ids(o, ids_g, "persistent bf16 cache", gap=BF16_GAP)
+    k.decode_forced(ids_g)
     assert g.cache_len() == k.cache_len() == 47
+    assert max_rel(g.logits(), o.logits()) < 2e-2
+    assert max_rel(g.logits(), k.logits()) < 1e-3
+    for layer in range(s["num_layers"]):
+        for pos in (0, 16, 17, 40):
+            kg, vg = g.kv(layer, 0, pos)
+            kk, vk = k.kv(layer, 0, pos)
+            ko, vo = o.kv(layer, 0, pos)
+            assert max_rel(kg, kk) < 1e-2 and max_rel(vg, vk) < 1e-2, (layer, pos)
+            assert max_rel(kg, ko) < 2e-2 and max_rel(vg, vo) < 2e-2, (layer, pos)
     g.close()
     k.close()
 
 
 @pytest.mark.parametrize("dims", [SMALL[0], SMALL[3]])
-def test_persistent_split_merge(tmp_path, dims, persist_kernel):
-    """max_seq 600 gives 19 attention chunks per head: the first kernel then
-    merges each head on four workgroups of head_dim / 4 columns. Prompt of 530
-    ids, 40 greedy steps, against the oracle."""
-    if persist_kernel == "stream":
-        pytest.skip("the streamed kernel merges per head on one wave")
+def test_persistent_split_merge(tmp_path, dims):
+    """max_seq 600 gives 19 attention chunks per head: the cooperative kernel
+    then merges each head on four workgroups of head_dim / 4 columns. Prompt
+    of 530 ids, 40 greedy steps, the oracle following."""
     s = shape_dict(*dims, 1e-6)
     t = random_map(s, seed=sum(dims) + 5, std=0.05)
     path = str(tmp_path / "m.safetensors")
     write_safetensors(path, t)
     max_seq = 600
-    g = myos.Model.open(path, to_block_shape(s), myos.KV_F32, max_seq)
-    if g.decode_path() != myos.DECODE_PERSISTENT:
-        g.close()
-        pytest.skip("the device cannot hold the cooperative decode grid")
+    g = open_persistent(path, s, myos.KV_F32, max_seq)
     o = oracle.Model(s, t, max_seq, threads=4)
     prompt = np.random.default_rng(13).integers(0, s["vocab"], 530)
     g.prefill(prompt)
     assert o.prefill(prompt) == 0
-    ids_g = g.greedy_decode(40)
-    ids_o, gaps = oracle_steps(o, 40)
-    n_ok = agree(ids_g, ids_o, gaps)
-    assert g.cache_len() == 570
-    if n_ok == 40:
-        assert_logits_parity(g.logits(), o.logits(), "split merge, after 40 steps")
-        assert max_rel(g.hidden(), o.hidden()) < 1e-4
+    follow_ids(o, g.greedy_decode(40), "split merge")
+    assert g.cache_len() == o.cache_len() == 570
+    assert_logits_parity(g.logits(), o.logits(), "split merge, after 40 steps")
+    assert max_rel(g.hidden(), o.hidden()) < 1e-4
+    check_kv(g, o, s, (0, 529, 530, 569), 1e-4)
     g.close()
 
 
@@ -192,50 +200,98 @@ def test_persistent_until_cache_full(tmp_path):
     t = random_map(s, seed=5, std=0.05)
     path = str(tmp_path / "m.safetensors")
     write_safetensors(path, t)
-    g = myos.Model.open(path, to_block_shape(s), myos.KV_F32, 12)
-    if g.decode_path() != myos.DECODE_PERSISTENT:
-        g.close()
-        pytest.skip("the device cannot hold the cooperative decode grid")
+    g = open_persistent(path, s, myos.KV_F32, 12)
     o = oracle.Model(s, t, 12, threads=2)
     g.prefill([3, 1, 4])
     assert o.prefill([3, 1, 4]) == 0
     with pytest.raises(myos.MyosError) as e:
         g.greedy_decode(20)
     assert e.value.code == myos.E_KV_FULL
-    ids_o, gaps = oracle_steps(o, 9)
-    assert agree(e.value.partial, ids_o, gaps) >= 0
     assert len(e.value.partial) == 9 and g.cache_len() == 12
+    follow_ids(o, e.value.partial, "until full")
+    assert_logits_parity(g.logits(), o.logits(), "at cache full")
+
+
+def test_persistent_wait_error_poisons_the_model(tmp_path):
+    """The error path of the bounded waits, forced from the host: with the
+    kernel's error word raised before the launch, every wait gives up at once
+    (the kernel still runs to its end), greedy_decode reports Hip and the
+    cursor stays; decode calls are then refused until a cache_clear +
+    prefill, after which decoding matches the oracle again."""
+    s = shape_dict(256, 4, 2, 64, 512, 1000, 2, 1e-6)
+    t = random_map(s, seed=7, std=0.05)
+    path = str(tmp_path / "m.safetensors")
+    write_safetensors(path, t)
+    g = open_persistent(path, s, myos.KV_F32, 40)
+    prompt = [5, 9, 2, 7]
+    g.prefill(prompt)
+    g.debug_raise_wait_error()
+    with pytest.raises(myos.MyosError) as e:
+        g.greedy_decode(6)
+    assert e.value.kind == "Hip" and g.cache_len() == 4
+    for call in (lambda: g.greedy_decode(1), lambda: g.forward_token(3, 4),
+                 lambda: g.decode_forced([3])):
+        with pytest.raises(myos.MyosError) as e:
+            call()
+        assert e.value.kind == "Hip" and g.cache_len() == 4
+    g.cache_clear()
+    g.prefill(prompt)
+    o = oracle.Model(s, t, 40, threads=2)
+    assert o.prefill(prompt) == 0
+    follow_ids(o, g.greedy_decode(10), "after recovery")
+    assert_logits_parity(g.logits(), o.logits(), "after recovery")
+    assert max_rel(g.hidden(), o.hidden()) < 1e-4
+    g.close()
+
+
+# -------------------------------------------------- Qwen2.5-1.5B shape ----
+
+Q15 = shape_dict(1536, 12, 2, 128, 8960, 151936, 28, 1e-6)
 
 
 @pytest.fixture(scope="module")
-def qwen15(tmp_path_factory):
-    path = os.environ.get("MYOS_TEST_WEIGHTS_1_5B")
-    if not path:
-        path = str(tmp_path_factory.mktemp("w") / "qwen25_1_5b_seed0.safetensors")
-        myos.write_random_qwen25(path, myos.preset(myos.SHAPE_QWEN25_1_5B), seed=0, std=0.02)
-    s = shape_dict(1536, 12, 2, 128, 8960, 151936, 28, 1e-6)
-    return path, s, oracle.load_safetensors_bits(path)
+def qwen15(qwen15_path):
+    return qwen15_path, Q15, oracle.load_safetensors_bits(qwen15_path)
 
 
-def test_persistent_qwen15_prefill128_greedy(qwen15):
-    """128 seeded prompt ids, then 12 greedy steps in one launch (seq 129..140,
-    five 32-position attention chunks per kv head)."""
+def test_persistent_qwen15_s1_128_greedy(qwen15):
+    """The bench's S1 workload: 128 seeded prompt ids, then all 128 greedy
+    steps in one launch (the 1.5B-specialised instantiation, f32 cache,
+    max_seq 256), every id under the tolerance rule with the oracle
+    following, then the final logits, hidden state and cache rows."""
     path, s, t = qwen15
     prompt = np.random.default_rng(2024).integers(0, 151936, 128)
-    g = myos.Model.open(path, myos.preset(myos.SHAPE_QWEN25_1_5B), myos.KV_F32, 256)
-    if g.decode_path() != myos.DECODE_PERSISTENT:
-        g.close()
-        pytest.skip("the device cannot hold the cooperative decode grid")
+    g = open_persistent(path, s, myos.KV_F32, 256)
     o = oracle.Model(s, t, 256, threads=16)
     g.prefill(prompt)
     assert o.prefill(prompt) == 0
-    ids_g = g.greedy_decode(12)
-    ids_o, gaps = oracle_steps(o, 12)
-    print("persistent ids", ids_g, "decode ms", g.last_decode_ms())
-    if agree(ids_g, ids_o, gaps) == 12:
-        assert_logits_parity(g.logits(), o.logits(), "after 12 persistent steps")
-        assert max_rel(g.hidden(), o.hidden()) < 1e-2
-        kg, vg = g.kv(27, 1, 139)
-        ko, vo = o.kv(27, 1, 139)
-        assert max_rel(kg, ko) < 1e-2 and max_rel(vg, vo) < 1e-2
+    assert_logits_parity(g.logits(), o.logits(), "prefill 128")
+    ids_g = g.greedy_decode(128)
+    exact = follow_ids(o, ids_g, "S1 persistent")
+    print(f"S1: {exact}/128 ids equal the oracle's own argmax; decode "
+          f"{g.last_decode_ms():.2f} ms")
+    assert g.cache_len() == o.cache_len() == 256
+    assert_logits_parity(g.logits(), o.logits(), "after 128 persistent steps")
+    assert max_rel(g.hidden(), o.hidden()) < 1e-2
+    assert max_rel(g.normed(), o.normed()) < 1e-2
+    check_kv(g, o, s, (0, 127, 128, 200, 255), 1e-2, heads=[0, 1])
+    g.close()
+
+
+def test_persistent_qwen15_s1_bf16_cache(qwen15):
+    """S1 with a bf16 KV cache (the 1.5B bf16 instantiation): 128 prompt ids,
+    48 greedy steps, the f32-cache oracle following at BF16_GAP."""
+    path, s, t = qwen15
+    prompt = np.random.default_rng(2024).integers(0, 151936, 128)
+    g = open_persistent(path, s, myos.KV_BF16, 256)
+    o = oracle.Model(s, t, 256, threads=16)
+    g.prefill(prompt)
+    assert o.prefill(prompt) == 0
+    assert max_rel(g.logits(), o.logits()) < 2e-2
+    exact = follow_ids(o, g.greedy_decode(48), "S1 bf16 cache", gap=BF16_GAP)
+    print(f"S1 bf16 cache: {exact}/48 ids equal the oracle's own argmax")
+    assert g.cache_len() == 176
+    assert max_rel(g.logits(), o.logits()) < 2e-2
+    assert max_rel(g.hidden(), o.hidden()) < 2e-2
+    check_kv(g, o, s, (0, 127, 175), 2e-2, heads=[1])
     g.close()
