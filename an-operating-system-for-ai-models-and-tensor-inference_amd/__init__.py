@@ -98,6 +98,7 @@ EXPORTS = {
     "myos_kv_bytes": ([P], SZ),
     "myos_write_random_qwen25": ([C.c_char_p, C.POINTER(BlockShape), C.c_uint64, F32, I32], I32),
     "myos_cache_clear": ([P], I32),
+    "myos_sha256_file": ([C.c_char_p, C.c_char_p], I32),
     "myos_time_kernel": ([P, I32, I32, C.POINTER(C.c_double)], I32),
     "myos_kernel_bytes": ([P, I32], C.c_double),
 }
@@ -416,6 +417,13 @@ class Model:
 
     def kv_bytes(self) -> int:
         return int(lib().myos_kv_bytes(self._h))
+
+
+def sha256_file(path: str) -> str:
+    """SHA-256 of a file (hex), the run fingerprint's model_sha256."""
+    out = C.create_string_buffer(65)
+    _check(lib().myos_sha256_file(os.fsencode(path), out), f"sha256 {path}")
+    return out.value.decode()
 
 
 def write_random_qwen25(path: str, shape: BlockShape | None = None, seed: int = 0,

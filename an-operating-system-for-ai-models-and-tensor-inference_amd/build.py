@@ -20,8 +20,8 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 SOURCES = ["myos_kernels.hip", "myos_persistent.hip", "myos_ops.cpp", "myos_model.cpp",
            "myos_safetensors.cpp",
-           "myos_gen.cpp"]
-CLI_SOURCES = ["myos_cli.cpp"]
+           "myos_gen.cpp", "myos_sha256.cpp"]
+CLI_SOURCES = ["myos_cli.cpp", "myos_arena.cpp"]
 
 COMMON = ["-O3", "-std=c++17", "-fPIC", "-Wall", f"--offload-arch={ARCH}",
           "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]

@@ -12,15 +12,27 @@
 //   --fingerprint-dir DIR             run_fingerprint.json, token_ids.txt and
 //                                     metrics.json go here (default runs/<id>)
 //
+//   --arena-s1 [--warmup W] [--repeats R]
+//                                     the W/R showdown harness (arena.rs): W + R
+//                                     fresh child processes, medians, DET and
+//                                     CORRECT gates (myos_arena.cpp); --steps
+//                                     defaults to 128 there
+//
 // and, for the device: --model-shape 1.5b|7b, --kv f32|bf16,
-// --decode-path auto|kernels|persistent. The arena protocol flags
-// (--arena-s1, --warmup, --repeats, --cost-card) drive a multi-process
-// benchmark harness outside the token loop and are refused.
+// --decode-path auto|kernels|persistent, --no-graph, and two verification
+// passes run after the timed decode (outside its timing): --gaps re-runs the
+// decode step by step and records every step's top-1 / top-2 logit gap;
+// --teacher-forced (with --ref-ids) feeds the reference ids instead and
+// reports how many steps' greedy ids agree with them. --no-hash leaves
+// model_sha256 null (the arena's children: the parent hashes once). The arena's llama.cpp
+// cost card (--cost-card) compares against a CPU competitor and is refused.
 //
 // run_fingerprint.json keeps the reference's fields (fingerprint.rs:161-203)
-// with device = the GPU; metrics.json keeps meter.rs:183-232's fields, with
-// t_prefill / t_decode from device events around the same boundaries
-// (main.rs:515-545), plus device fields.
+// with device = the GPU and model_sha256 = the weights file's SHA-256;
+// metrics.json keeps meter.rs:183-232's fields, with t_prefill / t_decode
+// around the same boundaries (main.rs:515-545) and M_peak from a 20 ms VmRSS
+// sampler (meter.rs:679-723), plus device fields: arch, HBM peak, algorithmic
+// bytes per decode token, achieved GB/s and the HBM roofline fraction.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include <stdio.h>
@@ -30,20 +42,27 @@
 #include <sys/stat.h>
 #include <unistd.h>
 
+#include <atomic>
 #include <chrono>
+#include <cmath>
 #include <fstream>
 #include <sstream>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include "../../include/myos_hip.h"
+#include "myos_arena.h"
 
 namespace {
 
 const char *kUsage =
     "myos [--weights PATH] [--block-fixture] [--steps N] [--threads N] [--fingerprint-dir DIR] "
-    "[--prompt-ids PATH] [--ref-ids PATH] [--model-shape 1.5b|7b] [--kv f32|bf16] "
-    "[--decode-path auto|kernels|persistent]";
+    "[--prompt-ids PATH] [--ref-ids PATH] [--arena-s1] [--warmup N] [--repeats N] "
+    "[--model-shape 1.5b|7b] [--kv f32|bf16] [--decode-path auto|kernels|persistent] "
+    "[--no-graph] [--gaps] [--teacher-forced] [--no-hash]";
+
+constexpr double kHbmPeakGBps = 8000.0;  // MI355X HBM3E
 
 struct Cli {
   std::string weights, fingerprint_dir, prompt_ids, ref_ids;
@@ -56,10 +75,15 @@ struct Cli {
   int shape = MYOS_SHAPE_QWEN25_1_5B;
   int kv = MYOS_KV_F32;
   int decode = MYOS_DECODE_AUTO;
+  bool has_shape = false, has_kv = false, has_decode = false;
+  bool arena = false, has_warmup = false, has_repeats = false;
+  size_t warmup = 3, repeats = 5;
+  bool no_graph = false, gaps = false, teacher = false, no_hash = false;
 };
 
 const char *flag_noun(const std::string &name) {
-  if (name == "--steps" || name == "--threads") return "a positive integer";
+  if (name == "--steps" || name == "--threads" || name == "--repeats") return "a positive integer";
+  if (name == "--warmup") return "a non-negative integer";
   if (name == "--model-shape") return "1.5b or 7b";
   if (name == "--kv") return "f32 or bf16";
   if (name == "--decode-path") return "auto, kernels or persistent";
@@ -110,9 +134,35 @@ int parse_cli(int argc, char **argv, Cli &c, std::string &err) {
       c.block_fixture = true;
       continue;
     }
-    if (arg == "--arena-s1" || arg.rfind("--warmup", 0) == 0 || arg.rfind("--repeats", 0) == 0 ||
-        arg.rfind("--cost-card", 0) == 0)
-      return err = arg + ": the arena protocol harness is not part of the device build", -1;
+    bool *sw = arg == "--arena-s1" ? &c.arena : arg == "--no-graph" ? &c.no_graph
+             : arg == "--gaps" ? &c.gaps : arg == "--teacher-forced" ? &c.teacher
+             : arg == "--no-hash" ? &c.no_hash : nullptr;
+    if (sw) {
+      if (*sw) return err = arg + " was given more than once", -1;
+      *sw = true;
+      continue;
+    }
+    if (arg.rfind("--cost-card", 0) == 0)
+      return err = arg + ": the llama.cpp cost card is not part of the device build", -1;
+    if ((r = match_flag(arg, "--warmup", i, argc, argv, v, err)) != 0) {
+      if (r < 0) return -1;
+      if (c.has_warmup) return err = "--warmup was given more than once", -1;
+      char *end = nullptr;
+      const unsigned long long n = strtoull(v.c_str(), &end, 10);
+      if (v.empty() || *end != '\0' || v[0] == '-')
+        return err = "--warmup needs a non-negative integer, got `" + v + "`", -1;
+      c.warmup = (size_t)n;
+      c.has_warmup = true;
+      continue;
+    }
+    if ((r = match_flag(arg, "--repeats", i, argc, argv, v, err)) != 0) {
+      if (r < 0) return -1;
+      if (c.has_repeats) return err = "--repeats was given more than once", -1;
+      if (!parse_positive(v, c.repeats))
+        return err = "--repeats needs a positive integer, got `" + v + "`", -1;
+      c.has_repeats = true;
+      continue;
+    }
     struct {
       const char *name;
       std::string *dst;
@@ -155,6 +205,7 @@ int parse_cli(int argc, char **argv, Cli &c, std::string &err) {
       if (v == "1.5b") c.shape = MYOS_SHAPE_QWEN25_1_5B;
       else if (v == "7b") c.shape = MYOS_SHAPE_QWEN25_7B;
       else return err = "--model-shape needs 1.5b or 7b, got `" + v + "`", -1;
+      c.has_shape = true;
       continue;
     }
     if ((r = match_flag(arg, "--kv", i, argc, argv, v, err)) != 0) {
@@ -162,6 +213,7 @@ int parse_cli(int argc, char **argv, Cli &c, std::string &err) {
       if (v == "f32") c.kv = MYOS_KV_F32;
       else if (v == "bf16") c.kv = MYOS_KV_BF16;
       else return err = "--kv needs f32 or bf16, got `" + v + "`", -1;
+      c.has_kv = true;
       continue;
     }
     if ((r = match_flag(arg, "--decode-path", i, argc, argv, v, err)) != 0) {
@@ -170,6 +222,7 @@ int parse_cli(int argc, char **argv, Cli &c, std::string &err) {
       else if (v == "kernels") c.decode = MYOS_DECODE_KERNELS;
       else if (v == "persistent") c.decode = MYOS_DECODE_PERSISTENT;
       else return err = "--decode-path needs auto, kernels or persistent, got `" + v + "`", -1;
+      c.has_decode = true;
       continue;
     }
     return err = "unknown argument `" + arg + "`", -1;
@@ -186,6 +239,17 @@ int parse_cli(int argc, char **argv, Cli &c, std::string &err) {
   if (c.has_prompt && !c.has_weights) return err = "--prompt-ids needs --weights", -1;
   if (c.has_prompt && c.block_fixture)
     return err = "--prompt-ids cannot be combined with --block-fixture", -1;
+  // main.rs:339-352
+  if (c.arena) {
+    if (c.block_fixture) return err = "--arena-s1 cannot be combined with --block-fixture", -1;
+    if (!c.has_weights) return err = "--arena-s1 needs --weights", -1;
+    if (!c.has_prompt) return err = "--arena-s1 needs --prompt-ids", -1;
+    if (!c.has_ref) return err = "--arena-s1 needs --ref-ids", -1;
+    if (!c.has_steps) c.steps = 128;
+  } else if (c.has_warmup || c.has_repeats) {
+    return err = "--warmup and --repeats need --arena-s1", -1;
+  }
+  if (c.teacher && !c.has_ref) return err = "--teacher-forced needs --ref-ids", -1;
   return 0;
 }
 
@@ -336,43 +400,135 @@ struct Run {
   std::vector<uint32_t> prompt, tokens;
   double t_load_s = 0, t_prefill_s = 0, t_decode_s = 0;
   double dev_prefill_ms = 0, dev_decode_ms = 0;
-  long rss_after_load = -1, peak = -1;
+  long rss_after_load = -1, peak = -1, hwm = -1;
   int decode_path = MYOS_DECODE_KERNELS;
   size_t weight_bytes = 0, kv_bytes = 0;
+  bool graph = true;
+  std::string sha256;  // empty: not hashed (block fixture) or unreadable
+  // verification pass (--gaps / --teacher-forced), outside the timed region
+  std::string verify_mode;
+  std::vector<uint32_t> verify_ids;  // greedy id of each step's input logits
+  std::vector<double> gaps;          // their top-1 / top-2 gap
 };
 
+// RssSampler, meter.rs:679-723: VmRSS polled every 20 ms on a thread; the
+// peak is the largest sample (taken from after load to after decode)
+struct RssSampler {
+  std::atomic<bool> stop{false};
+  std::atomic<long> peak{-1};
+  std::thread th;
+  void start() {
+    peak = proc_kib("VmRSS:");
+    th = std::thread([this] {
+      while (!stop.load()) {
+        const long v = proc_kib("VmRSS:");
+        if (v > peak.load()) peak = v;
+        std::this_thread::sleep_for(std::chrono::milliseconds(20));
+      }
+    });
+  }
+  long finish() {
+    stop = true;
+    if (th.joinable()) th.join();
+    const long v = proc_kib("VmRSS:");
+    return v > peak.load() ? v : peak.load();
+  }
+};
+
+// greedy id and top-1 / top-2 gap of the logits the last forward left
+int logits_top2(myos_model *m, size_t vocab, std::vector<float> &buf, uint32_t *id, double *gap) {
+  buf.resize(vocab);
+  int rc = myos_copy_logits(m, buf.data(), vocab);
+  if (rc) return rc;
+  // greedy_token (model_core/src/lib.rs:157-167): strict >, lowest index on ties
+  float best = -INFINITY;
+  uint32_t bi = 0;
+  for (size_t i = 0; i < vocab; i++)
+    if (buf[i] > best) best = buf[i], bi = (uint32_t)i;
+  float second = -INFINITY;
+  for (size_t i = 0; i < vocab; i++)
+    if (i != bi && buf[i] > second) second = buf[i];
+  *id = bi;
+  *gap = (double)best - (double)second;
+  return MYOS_OK;
+}
+
 // decode_bf16_timed (main.rs:515-545): open (t_load), then prefill (t_prefill,
-// ending before the first new token), then greedy_decode (t_decode)
-int decode_timed(const std::string &path, const myos_block_shape &shape, int kv, int mode,
-                 Run &r) {
+// ending before the first new token), then greedy_decode (t_decode); then,
+// untimed, the verification pass when asked for
+int decode_timed(const std::string &path, const myos_block_shape &shape, const Cli &c,
+                 const std::vector<uint32_t> *teacher, Run &r) {
   using clk = std::chrono::steady_clock;
   const size_t max_seq = r.prompt.size() + r.tokens.size();
   myos_model *m = nullptr;
   auto t0 = clk::now();
-  int rc = myos_model_open(path.c_str(), &shape, kv, max_seq, &m);
+  int rc = myos_model_open(path.c_str(), &shape, c.kv, max_seq, &m);
   if (rc) return rc;
   r.t_load_s = std::chrono::duration<double>(clk::now() - t0).count();
   r.rss_after_load = proc_kib("VmRSS:");
-  if (mode != MYOS_DECODE_AUTO && (rc = myos_set_decode_mode(m, mode)) != MYOS_OK) {
+  if (c.decode != MYOS_DECODE_AUTO && (rc = myos_set_decode_mode(m, c.decode)) != MYOS_OK) {
     myos_model_close(m);
     return rc;
   }
+  if (c.no_graph && (rc = myos_set_graph(m, 0)) != MYOS_OK) {
+    myos_model_close(m);
+    return rc;
+  }
+  r.graph = !c.no_graph;
   r.decode_path = myos_decode_path(m);
+  RssSampler rss;
+  rss.start();
   auto t1 = clk::now();
   rc = myos_prefill(m, r.prompt.data(), r.prompt.size());
   if (!rc) rc = myos_stream_sync(nullptr);
   auto t2 = clk::now();
   if (!rc) rc = myos_greedy_decode(m, r.tokens.size(), r.tokens.data());
   auto t3 = clk::now();
+  r.peak = rss.finish();
   r.t_prefill_s = std::chrono::duration<double>(t2 - t1).count();
   r.t_decode_s = std::chrono::duration<double>(t3 - t2).count();
   r.dev_prefill_ms = myos_last_prefill_ms(m);
   r.dev_decode_ms = myos_last_decode_ms(m);
   r.weight_bytes = myos_weight_bytes(m);
   r.kv_bytes = myos_kv_bytes(m);
-  r.peak = proc_kib("VmHWM:");
+  if (!rc && (c.gaps || c.teacher)) {
+    // the same decode again, one step per call, reading each step's logits:
+    // fed the reference ids (--teacher-forced) or its own greedy ids
+    r.verify_mode = c.teacher ? "teacher-forced" : "greedy";
+    rc = myos_cache_clear(m);
+    if (!rc) rc = myos_prefill(m, r.prompt.data(), r.prompt.size());
+    std::vector<float> buf;
+    for (size_t i = 0; !rc && i < r.tokens.size(); i++) {
+      uint32_t id;
+      double gap;
+      rc = logits_top2(m, shape.vocab, buf, &id, &gap);
+      if (rc) break;
+      r.verify_ids.push_back(id);
+      r.gaps.push_back(gap);
+      uint32_t out;
+      if (c.teacher) {
+        const uint32_t feed = i < teacher->size() ? (*teacher)[i] : id;
+        rc = myos_decode_forced(m, &feed, 1, &out);
+      } else {
+        rc = myos_greedy_decode(m, 1, &out);
+      }
+    }
+  }
+  r.hwm = proc_kib("VmHWM:");
   myos_model_close(m);
   return rc;
+}
+
+// algorithmic HBM bytes of one decode token at sequence length seq: every
+// bf16 weight the step streams (all layers, final norm, the head, one embed
+// row) plus the K/V rows attention reads
+double decode_token_bytes(const myos_block_shape &s, double seq, int kv) {
+  const double H = (double)s.hidden, I = (double)s.intermediate, V = (double)s.vocab;
+  const double Q = (double)(s.num_q_heads * s.head_dim), KD = (double)(s.num_kv_heads * s.head_dim);
+  const double per_layer = 2 * H + Q * H + Q + 2 * (KD * H + KD) + H * Q + 3 * I * H;
+  const double w = 2 * ((double)s.num_layers * per_layer + H + V * H + H);
+  const double kvb = (double)s.num_layers * 2 * KD * seq * (kv == MYOS_KV_BF16 ? 2 : 4);
+  return w + kvb;
 }
 
 int write_text(const std::string &dir, const char *name, const std::string &text) {
@@ -390,7 +546,7 @@ std::string fingerprint_json(const Cli &c, const myos_block_shape &s, bool weigh
   const char *dp = r.decode_path == MYOS_DECODE_PERSISTENT ? "persistent" : "kernels";
   std::vector<std::pair<std::string, std::string>> f = {
       {"model_id", model_id},
-      {"model_sha256", "null"},
+      {"model_sha256", r.sha256.empty() ? "null" : json_str(r.sha256)},
       {"fmt", json_str(weights ? "safetensors" : "in-process")},
       {"quant_or_dtype", json_str("bf16")},
       {"acc_path", json_str("bf16_w_fp32_acc")},
@@ -416,10 +572,11 @@ std::string fingerprint_json(const Cli &c, const myos_block_shape &s, bool weigh
       {"decode_path", json_str(dp)},
       {"kv_dtype", json_str(c.kv == MYOS_KV_BF16 ? "bf16" : "f32")},
       {"build", json_str(myos_build_info())},
+      {"graph", r.graph ? "true" : "false"},
       {"notes", json_str("Device run: weights uploaded once to HBM, prefill on MFMA (bf16 hi/lo "
                          "activation split), greedy decode on the GPU. threads is the recorded "
                          "--threads value; the device path has no host GEMV workers. "
-                         "model_sha256 is null: the file is not hashed.")},
+                         "model_sha256 is the SHA-256 of the weights file.")},
   };
   std::string o = "{\n";
   for (size_t i = 0; i < f.size(); i++)
@@ -427,9 +584,39 @@ std::string fingerprint_json(const Cli &c, const myos_block_shape &s, bool weigh
   return o + "}\n";
 }
 
+std::string arch_name() {
+  hipDeviceProp_t p;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || hipGetDeviceProperties(&p, dev) != hipSuccess)
+    return "unknown";
+  std::string a = p.gcnArchName;
+  return a.substr(0, a.find(':'));
+}
+
 // metrics.json (meter.rs:183-232 + derive :48-78) + device fields
-std::string metrics_json(const Cli &c, const Run &r, int correct) {
+std::string metrics_json(const Cli &c, const myos_block_shape &shape, const Run &r, int correct,
+                         const std::vector<uint32_t> *ref) {
   const double n_gen = (double)r.tokens.size(), n_prompt = (double)r.prompt.size();
+  // bytes per decode token averaged over the steps (sequence n_prompt + 1 ..
+  // n_prompt + n_gen), and what the device moved at its decode rate
+  const double b_tok = decode_token_bytes(shape, n_prompt + (n_gen + 1) / 2, c.kv);
+  const double dev_tok_s = r.dev_decode_ms > 0 ? n_gen / (r.dev_decode_ms * 1e-3) : 0;
+  const double gbps = b_tok * dev_tok_s / 1e9;
+  std::string gaps = "[", vids = "[";
+  double min_gap = INFINITY;
+  size_t agree = 0;
+  long first_diff = -1;
+  const std::vector<uint32_t> &want = r.verify_mode == "teacher-forced" && ref ? *ref : r.tokens;
+  for (size_t i = 0; i < r.gaps.size(); i++) {
+    gaps += (i ? ", " : "") + json_num(r.gaps[i]);
+    vids += (i ? ", " : "") + std::to_string(r.verify_ids[i]);
+    min_gap = std::min(min_gap, r.gaps[i]);
+    if (i < want.size() && r.verify_ids[i] == want[i]) agree++;
+    else if (first_diff < 0) first_diff = (long)i;
+  }
+  gaps += "]";
+  vids += "]";
+  const bool verified = !r.verify_mode.empty();
   auto mib = [](long k) { return k < 0 ? std::string("null") : json_num(k / 1024.0); };
   auto kib = [](long k) { return k < 0 ? std::string("null") : std::to_string(k); };
   std::vector<std::pair<std::string, std::string>> f = {
@@ -457,17 +644,38 @@ std::string metrics_json(const Cli &c, const Run &r, int correct) {
       {"M_rss_after_load_MiB", mib(r.rss_after_load)},
       {"correct", correct < 0 ? "null" : correct ? "true" : "false"},
       {"device", json_str(device_name())},
+      {"arch", json_str(arch_name())},
+      {"model_sha256", r.sha256.empty() ? "null" : json_str(r.sha256)},
+      {"kv_dtype", json_str(c.kv == MYOS_KV_BF16 ? "bf16" : "f32")},
+      {"graph", r.graph ? "true" : "false"},
+      {"hbm_peak_GBps", json_num(kHbmPeakGBps)},
+      {"decode_bytes_per_token", json_num(b_tok)},
+      {"achieved_GBps", dev_tok_s > 0 ? json_num(gbps) : "null"},
+      {"roofline_frac", dev_tok_s > 0 ? json_num(gbps / kHbmPeakGBps) : "null"},
+      {"device_prefill_tok_s", r.dev_prefill_ms > 0 ? json_num(n_prompt / (r.dev_prefill_ms * 1e-3)) : "null"},
       {"device_prefill_ms", json_num(r.dev_prefill_ms)},
       {"device_decode_ms", json_num(r.dev_decode_ms)},
       {"device_decode_tok_s", r.dev_decode_ms > 0 ? json_num(n_gen / (r.dev_decode_ms * 1e-3)) : "null"},
       {"device_weight_bytes", std::to_string(r.weight_bytes)},
       {"device_kv_bytes", std::to_string(r.kv_bytes)},
       {"decode_path", json_str(r.decode_path == MYOS_DECODE_PERSISTENT ? "persistent" : "kernels")},
+      {"M_hwm_KiB", kib(r.hwm)},
+      {"verify_mode", verified ? json_str(r.verify_mode) : "null"},
+      {"verify_agree", verified ? std::to_string(agree) : "null"},
+      {"verify_first_diff", verified && first_diff >= 0 ? std::to_string(first_diff) : "null"},
+      {"min_top2_gap", verified && !r.gaps.empty() ? json_num(min_gap) : "null"},
+      {"verify_ids", verified ? vids : "null"},
+      {"top2_gap_per_step", verified ? gaps : "null"},
       {"timing", json_str("t_load is weight open+parse+upload to HBM and is outside L_prefill and "
                           "T_decode. t_prefill is the prompt prefill (KV and workspace are "
                           "allocated at load) and ends before the first new token. t_decode is "
                           "greedy_decode of n_gen new tokens. device_* are hipEvent times of the "
-                          "same two phases. M_peak is VmHWM of the process.")},
+                          "same two phases. M_peak is the largest VmRSS sample of a 20 ms poll "
+                          "from after load to after decode; M_hwm is the kernel's VmHWM. "
+                          "roofline_frac = decode_bytes_per_token x device decode tok/s / "
+                          "hbm_peak. The verify_* fields come from a second, untimed pass one "
+                          "step per call: verify_ids[i] is the greedy id of step i's input "
+                          "logits and top2_gap_per_step[i] their top-1 / top-2 gap.")},
   };
   std::string o = "{\n";
   for (size_t i = 0; i < f.size(); i++)
@@ -492,6 +700,44 @@ int main(int argc, char **argv) {
   if (!c.block_fixture && !c.has_weights) {
     fprintf(stderr, "MyOS: nothing to decode: pass --weights PATH (or MYOS_WEIGHTS) or --block-fixture\nusage: %s\n", kUsage);
     return 2;
+  }
+  if (c.arena) {
+    // run_arena_cli, main.rs:694-794: this process only spawns and reads
+    // children, and never initialises the GPU
+    std::vector<uint32_t> prompt;
+    if (read_token_ids(c.prompt_ids, prompt, err)) {
+      fprintf(stderr, "MyOS prompt-ids: %s\n", err.c_str());
+      return 1;
+    }
+    myos_cli::ArenaJob job;
+    char exe[4096];
+    const ssize_t n = readlink("/proc/self/exe", exe, sizeof exe - 1);
+    if (n <= 0) {
+      fprintf(stderr, "MyOS arena: cannot resolve this executable\n");
+      return 1;
+    }
+    exe[n] = '\0';
+    job.bin = exe;
+    job.weights = c.weights;
+    job.prompt_ids = c.prompt_ids;
+    job.ref_ids = c.ref_ids;
+    job.steps = c.steps;
+    job.threads = c.threads;
+    job.warmup = c.warmup;
+    job.repeats = c.repeats;
+    job.out_dir = c.has_fp ? c.fingerprint_dir
+                           : "runs/s1-myos-hip-bf16-t" + std::to_string(c.threads);
+    if (c.has_shape) job.device_args.push_back(c.shape == MYOS_SHAPE_QWEN25_7B ? "--model-shape=7b" : "--model-shape=1.5b");
+    if (c.has_kv) job.device_args.push_back(c.kv == MYOS_KV_BF16 ? "--kv=bf16" : "--kv=f32");
+    if (c.has_decode)
+      job.device_args.push_back(c.decode == MYOS_DECODE_PERSISTENT ? "--decode-path=persistent"
+                                : c.decode == MYOS_DECODE_KERNELS ? "--decode-path=kernels"
+                                                                   : "--decode-path=auto");
+    if (c.no_graph) job.device_args.push_back("--no-graph");
+    job.device_args.push_back("--no-hash");
+    char hex[65];
+    if (myos_sha256_file(c.weights.c_str(), hex) == MYOS_OK) job.model_sha256 = hex;
+    return myos_cli::run_arena(job, ref);
   }
 
   Run r;
@@ -527,7 +773,17 @@ int main(int argc, char **argv) {
     }
   }
   r.tokens.assign(c.steps, 0);
-  const int rc = decode_timed(path, shape, c.kv, c.decode, r);
+  // the weights file is hashed on a thread while the run goes on
+  std::string sha;
+  std::thread hasher;
+  if (weights && !c.no_hash)
+    hasher = std::thread([&sha, path] {
+      char hex[65];
+      if (myos_sha256_file(path.c_str(), hex) == MYOS_OK) sha = hex;
+    });
+  const int rc = decode_timed(path, shape, c, c.has_ref ? &ref : nullptr, r);
+  if (hasher.joinable()) hasher.join();
+  r.sha256 = sha;
   if (c.block_fixture) unlink(tmpl);
   if (rc) {
     if (c.block_fixture)
@@ -556,7 +812,7 @@ int main(int argc, char **argv) {
       }
     }
     const int correct = c.has_ref ? correct_line(r.tokens, ref) == "CORRECT: PASS" : -1;
-    if (write_text(dir, "metrics.json", metrics_json(c, r, correct))) {
+    if (write_text(dir, "metrics.json", metrics_json(c, shape, r, correct, c.has_ref ? &ref : nullptr))) {
       fprintf(stderr, "MyOS metrics: cannot write %s/metrics.json\n", dir.c_str());
       return 1;
     }
@@ -566,5 +822,21 @@ int main(int argc, char **argv) {
     printf("MyOS Phase1 block fixture (prompt=0): %s\n", ids_list(r.tokens).c_str());
   }
   if (c.has_ref) printf("%s\n", correct_line(r.tokens, ref).c_str());
+  if (c.teacher) {
+    // each step fed ref[i]; its greedy id compared with ref[i] (the id the
+    // reference chose from the same prefix), with this run's top-2 gap there
+    size_t agree = 0;
+    long first = -1;
+    for (size_t i = 0; i < r.verify_ids.size(); i++) {
+      if (i < ref.size() && r.verify_ids[i] == ref[i]) agree++;
+      else if (first < 0) first = (long)i;
+    }
+    if (first < 0)
+      printf("TEACHER-FORCED: PASS %zu/%zu\n", agree, r.verify_ids.size());
+    else
+      printf("TEACHER-FORCED: %zu/%zu first_diff@%ld: got=%u ref=%u gap=%.6g\n", agree,
+             r.verify_ids.size(), first, r.verify_ids[first],
+             (size_t)first < ref.size() ? ref[first] : 0u, r.gaps[first]);
+  }
   return 0;
 }

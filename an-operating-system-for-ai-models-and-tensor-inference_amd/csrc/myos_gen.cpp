@@ -48,14 +48,20 @@ inline uint16_t bf16_rne(float f) {
   return (uint16_t)(u >> 16);
 }
 
+// elements [i0, i1) into out[0, i1 - i0); each Box-Muller pair's radius and
+// angle are evaluated once for both of its elements
 void fill_normal(uint16_t *out, size_t i0, size_t i1, uint64_t key, float std_dev) {
   const double two_pi = 6.283185307179586476925286766559;
-  for (size_t i = i0; i < i1; i++) {
+  for (size_t i = i0; i < i1;) {
     const uint64_t j = i / 2;
     const double r = sqrt(-2.0 * log(1.0 - unit(key, 2 * j)));
     const double a = two_pi * unit(key, 2 * j + 1);
-    const double z = (i & 1) ? r * sin(a) : r * cos(a);
-    out[i - i0] = bf16_rne((float)((double)std_dev * z));
+    if (!(i & 1)) {
+      out[i - i0] = bf16_rne((float)((double)std_dev * (r * cos(a))));
+      if (++i == i1) break;
+    }
+    out[i - i0] = bf16_rne((float)((double)std_dev * (r * sin(a))));
+    i++;
   }
 }
 

@@ -8,11 +8,13 @@ ids prefilled (MFMA GEMMs), then 128 greedy decode steps (one cooperative
 kernel launch on the default path), batch 1, max_seq 256, f32 KV cache.
 
 Prints one JSON line: value = decode tokens/s over the timed steps (weights
-already resident in HBM), prefill tok/s beside it, the decode HBM-roofline
-fraction (weights + KV bytes per token / 8 TB/s), the live roofline of the
+already resident in HBM), prefill tok/s beside it, the decode and prefill
+HBM-roofline fractions (bytes per token / 8 TB/s), the live roofline of the
 dominant kernel (the cooperative decode kernel, timed with hipEvents on the
-model's stream), and the CPU oracle timed on a bounded sample of the same
-workload on the host cores.
+model's stream), the parity of the timed run against the oracle, the
+fresh-process W/R medians of the CLI's arena harness, and the CPU oracle on
+the same workload (medians, host core count and 8 threads). The host-only
+legs (oracle, arena children) run before this process touches the GPU.
 """
 from __future__ import annotations
 
@@ -38,12 +40,17 @@ def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def host_cores() -> int:
+def host_nproc() -> int:
     try:
-        n = len(os.sched_getaffinity(0))
+        return len(os.sched_getaffinity(0))
     except AttributeError:
-        n = os.cpu_count() or 1
-    return max(1, min(16, n))  # one GPU's share of the host
+        return os.cpu_count() or 1
+
+
+def host_cores() -> int:
+    # the reference caps --threads at 64 (gemv_bf16_kernel.rs:34,
+    # main.rs:416-424); a GPU box allots 16 host cores per GPU
+    return max(1, min(16, host_nproc(), 64))
 
 
 def weight_bytes(s) -> int:
@@ -104,36 +111,112 @@ def gemv_microbench(reps=5):
     return out
 
 
-def cpu_baseline(path, shape, prompt, n_steps, gpu_ids):
+def _oracle_shape(shape):
+    return dict(hidden=shape.hidden, num_q_heads=shape.num_q_heads,
+                num_kv_heads=shape.num_kv_heads, head_dim=shape.head_dim,
+                intermediate=shape.intermediate, vocab=shape.vocab,
+                num_layers=shape.num_layers, rms_eps=np.float32(shape.rms_eps),
+                rope_theta=np.float32(shape.rope_theta))
+
+
+def cpu_baseline(path, shape, prompt, n_steps, repeats):
+    """The oracle (the C restatement of the reference's CPU path: AVX2 32-row
+    GEMV over a row-span thread pool, serial attention) on the same weights
+    and prompt: prefill, then n_steps greedy steps, `repeats` scored runs
+    after one short warm-up, at the host core count and at 8 threads.
+    Medians (meter.rs:86-98); also each step's greedy id and top-1 / top-2
+    gap and the final logits, for the parity fields of the bench line."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle
-    sd = dict(hidden=shape.hidden, num_q_heads=shape.num_q_heads,
-              num_kv_heads=shape.num_kv_heads, head_dim=shape.head_dim,
-              intermediate=shape.intermediate, vocab=shape.vocab,
-              num_layers=shape.num_layers, rms_eps=np.float32(shape.rms_eps),
-              rope_theta=np.float32(shape.rope_theta))
+    sd = _oracle_shape(shape)
     t = oracle.load_safetensors_bits(path)
-    cores = host_cores()
     out = {}
-    for threads in sorted({cores, 8}, reverse=True):
+    ref = None
+    for threads in sorted({host_cores(), 8}, reverse=True):
         m = oracle.Model(sd, t, len(prompt) + n_steps, threads=threads)
-        t0 = time.perf_counter()
-        assert m.prefill(prompt) == 0
-        t1 = time.perf_counter()
-        rc, ids = m.greedy_decode(n_steps)
-        t2 = time.perf_counter()
-        assert rc == 0
-        out[threads] = dict(prefill_s=t1 - t0, decode_s=t2 - t1, ids=[int(v) for v in ids])
-        log(f"cpu oracle threads={threads}: prefill {len(prompt)} in {t1 - t0:.2f}s, "
-            f"{n_steps} decode in {t2 - t1:.2f}s")
+        assert m.prefill(prompt[:8]) == 0  # warm-up: the pool and the weight pages
+        pre, dec = [], []
+        for r in range(repeats):
+            m = oracle.Model(sd, t, len(prompt) + n_steps, threads=threads)
+            t0 = time.perf_counter()
+            assert m.prefill(prompt) == 0
+            t1 = time.perf_counter()
+            ids, gaps = [], []
+            for _ in range(n_steps):
+                lg = m.logits()
+                tok = int(oracle.greedy_token(lg))
+                if ref is None:
+                    srt = np.sort(lg.astype(np.float64))
+                    gaps.append(float(srt[-1] - srt[-2]))
+                ids.append(tok)
+                assert m.forward_token(tok, m.cache_len()) == 0
+            t2 = time.perf_counter()
+            pre.append(t1 - t0)
+            dec.append(t2 - t1)
+            if ref is None:
+                ref = dict(ids=ids, gaps=gaps, final_logits=m.logits())
+            log(f"cpu oracle threads={threads} run {r + 1}/{repeats}: prefill {len(prompt)} in "
+                f"{t1 - t0:.2f}s, {n_steps} decode in {t2 - t1:.2f}s")
+        out[threads] = dict(prefill_s=float(np.median(pre)), decode_s=float(np.median(dec)))
         del m
-    ids = out[cores]["ids"]
-    match = 0
-    for a, b in zip(ids, gpu_ids):
-        if a != b:
-            break
-        match += 1
-    return cores, out, match
+    return out, ref
+
+
+def run_arena(path, shape_name, prompt, ref_ids, n_steps, kv, warmup, repeats):
+    """The CLI's --arena-s1 harness (W warm-up + R scored fresh processes,
+    medians, DET / CORRECT gates against the oracle's ids), started before
+    this process touches the GPU."""
+    import subprocess
+    import tempfile
+    d = tempfile.mkdtemp(prefix="myos_arena_")
+    pp, rp = os.path.join(d, "prompt.txt"), os.path.join(d, "ref.txt")
+    with open(pp, "w") as f:
+        f.write(" ".join(str(int(v)) for v in prompt) + "\n")
+    with open(rp, "w") as f:
+        f.write(" ".join(str(int(v)) for v in ref_ids) + "\n")
+    cmd = [myos.CLI_PATH, "--arena-s1", "--weights", path, "--prompt-ids", pp, "--ref-ids", rp,
+           "--steps", str(n_steps), "--warmup", str(warmup), "--repeats", str(repeats),
+           "--model-shape", shape_name, "--kv", kv, "--fingerprint-dir", os.path.join(d, "run")]
+    t0 = time.perf_counter()
+    r = subprocess.run(cmd, capture_output=True, text=True, timeout=900)
+    log(f"arena W={warmup} R={repeats} in {time.perf_counter() - t0:.1f}s: "
+        f"{r.stdout.strip().splitlines()[0] if r.stdout.strip() else r.stderr[-300:]}")
+    agg_path = os.path.join(d, "run", "metrics.json")
+    if not os.path.exists(agg_path):
+        return {"error": (r.stderr or r.stdout)[-400:], "exit": r.returncode}
+    agg = json.load(open(agg_path))
+    return {"W": agg["W"], "R": agg["R"], "det": agg["det"], "correct": agg["CORRECT"],
+            "median": agg["median"], "min": agg["min"], "max": agg["max"],
+            "exit": r.returncode, "run_dir": os.path.join(d, "run")}
+
+
+def bench_prompt(shape, n):
+    return np.random.default_rng(2024).integers(0, shape.vocab, n).astype(np.uint32)
+
+
+def host_legs(args, is7b, path, n_cpu):
+    """The child process of the host-only legs: writes the weights file if it
+    is missing, then runs the CPU baseline and the arena; results go to
+    <dir>/host.json and <dir>/ref_logits.npy."""
+    shape = myos.preset(myos.SHAPE_QWEN25_7B if is7b else myos.SHAPE_QWEN25_1_5B)
+    if not os.path.exists(path):
+        os.makedirs(os.path.dirname(path), exist_ok=True)
+        log(f"writing random-init weights to {path}")
+        t0 = time.perf_counter()
+        myos.write_random_qwen25(path, shape, seed=0, std=0.02, threads=host_cores())
+        log(f"weights written in {time.perf_counter() - t0:.1f}s")
+    prompt = bench_prompt(shape, args.prompt)
+    cpu_res, ref = None, None
+    if not args.no_cpu_baseline:
+        cpu_res, ref = cpu_baseline(path, shape, prompt, n_cpu, args.cpu_repeats)
+    arena = None
+    if not args.no_arena and ref is not None and n_cpu == args.decode:
+        arena = run_arena(path, "7b" if is7b else "1.5b", prompt, ref["ids"], args.decode,
+                          args.kv, args.arena_warmup, args.arena_repeats)
+    if ref is not None:
+        np.save(os.path.join(args.host_legs, "ref_logits.npy"), ref.pop("final_logits"))
+    with open(os.path.join(args.host_legs, "host.json"), "w") as f:
+        json.dump({"cpu": cpu_res, "ref": ref, "arena": arena}, f)
 
 
 def main():
@@ -145,36 +228,61 @@ def main():
     ap.add_argument("--decode", type=int, default=128)
     ap.add_argument("--kv", choices=["f32", "bf16"], default="f32")
     ap.add_argument("--weights", default=os.environ.get("MYOS_BENCH_WEIGHTS"))
-    ap.add_argument("--cpu-decode-steps", type=int, default=16)
+    ap.add_argument("--cpu-decode-steps", type=int, default=None,
+                    help="greedy steps of the CPU baseline (default: all --decode steps)")
+    ap.add_argument("--cpu-repeats", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--arena-warmup", type=int, default=3)
+    ap.add_argument("--arena-repeats", type=int, default=5)
+    ap.add_argument("--no-arena", action="store_true")
     ap.add_argument("--kernel-reps", type=int, default=20)
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--decode-path", choices=["auto", "kernels", "persistent"], default="auto")
     ap.add_argument("--no-gemv-microbench", action="store_true")
     ap.add_argument("--shape", choices=["qwen2.5-1.5b", "qwen2.5-7b"], default="qwen2.5-1.5b",
                     help="model shape (the headline metric is quoted on qwen2.5-1.5b)")
+    ap.add_argument("--host-legs", metavar="DIR", help=argparse.SUPPRESS)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: every box here has one MI355X and this build has "
               f"no multi-GPU path (--gpus {args.gpus} requested)", file=sys.stderr)
         sys.exit(2)
 
-    if not args.no_gemv_microbench:
-        # torch carries its own HIP runtime: it must initialise the device before
-        # the library's runtime does (the microbench allocates through torch)
-        import torch
-        torch.cuda.init()
     is7b = args.shape == "qwen2.5-7b"
-    shape = myos.preset(myos.SHAPE_QWEN25_7B if is7b else myos.SHAPE_QWEN25_1_5B)
     path = args.weights or ("/tmp/myos_bench/qwen25_7b_seed0.safetensors" if is7b
                             else "/tmp/myos_bench/qwen25_1_5b_seed0.safetensors")
-    if not os.path.exists(path):
-        os.makedirs(os.path.dirname(path), exist_ok=True)
-        log(f"writing random-init weights to {path}")
-        t0 = time.perf_counter()
-        myos.write_random_qwen25(path, shape, seed=0, std=0.02, threads=host_cores())
-        log(f"weights written in {time.perf_counter() - t0:.1f}s")
+    n_cpu = args.cpu_decode_steps or args.decode
+    if args.host_legs:
+        host_legs(args, is7b, path, n_cpu)
+        return
 
+    # The host-only legs run in a child process before this one touches the
+    # GPU: the weights file (if missing), the CPU baseline (the oracle) and the
+    # fresh-process arena runs. This process then initialises torch's HIP
+    # runtime before it loads the library (the microbench allocates through
+    # torch, whose runtime has to come up first).
+    import subprocess
+    import tempfile
+    hdir = tempfile.mkdtemp(prefix="myos_bench_host_")
+    cmd = [sys.executable, "-u", os.path.abspath(__file__), "--host-legs", hdir] + sys.argv[1:]
+    t0 = time.perf_counter()
+    r = subprocess.run(cmd)
+    if r.returncode != 0:
+        log(f"host legs failed (exit {r.returncode})")
+        sys.exit(r.returncode)
+    host = json.load(open(os.path.join(hdir, "host.json")))
+    log(f"host legs done in {time.perf_counter() - t0:.1f}s")
+    cpu_res = {int(k): v for k, v in host["cpu"].items()} if host["cpu"] else None
+    ref = host["ref"]
+    if ref is not None:
+        ref["final_logits"] = np.load(os.path.join(hdir, "ref_logits.npy"))
+    arena = host["arena"]
+
+    if not args.no_gemv_microbench:
+        import torch
+        torch.cuda.init()
+    shape = myos.preset(myos.SHAPE_QWEN25_7B if is7b else myos.SHAPE_QWEN25_1_5B)
+    prompt = bench_prompt(shape, args.prompt)
     max_seq = args.prompt + args.decode
     kv = myos.KV_BF16 if args.kv == "bf16" else myos.KV_F32
     t0 = time.perf_counter()
@@ -187,8 +295,6 @@ def main():
                        "persistent": myos.DECODE_PERSISTENT}[args.decode_path])
     path_name = "persistent" if m.decode_path() == myos.DECODE_PERSISTENT else "kernels"
     log(f"decode path: {path_name}")
-    rng = np.random.default_rng(2024)
-    prompt = rng.integers(0, shape.vocab, args.prompt).astype(np.uint32)
 
     def step():
         m.cache_clear()
@@ -221,6 +327,46 @@ def main():
     seqs = np.arange(args.prompt + 1, args.prompt + args.decode + 1)
     b_tok = wb + float(np.mean([kv_bytes_per_token(shape, int(q), skv) for q in seqs]))
     decode_frac = decode_tok_s * b_tok / HBM_PEAK
+    # prefill: every projection weight byte once, the head once (last id), and
+    # the cache rows written
+    prefill_bytes = wb - 2 * shape.hidden + kv_bytes_per_token(shape, args.prompt, skv)
+    prefill_ms = dp / args.steps
+    pf_roof = {"bound": "hbm", "bytes": int(prefill_bytes), "avg_ms": round(prefill_ms, 4),
+               "achieved_GBps": round(prefill_bytes / (prefill_ms * 1e-3) / 1e9, 1),
+               "frac": round(prefill_bytes / (prefill_ms * 1e-3) / HBM_PEAK, 4)}
+
+    # parity of the timed run: the GPU ids under the tolerance rule against
+    # the oracle's (each step's top-1 / top-2 gap), then both decode paths
+    # teacher-forced with the oracle's ids against the oracle's final logits:
+    # the cooperative kernel multiplies gate/up, the down partials and the
+    # head with v_dot2 over the activations split into bf16 hi + lo (16
+    # significant bits); the per-kernel path keeps f32 activations
+    parity = None
+    if ref is not None and n_cpu == args.decode:
+        agree, first_div = 0, None
+        for i, (a, b) in enumerate(zip(ids0, ref["ids"])):
+            if a != b:
+                first_div = {"step": i, "oracle_gap": ref["gaps"][i]}
+                break
+            agree += 1
+        o_lg = ref["final_logits"]
+        rel = {}
+        for name, mode in (("persistent", myos.DECODE_PERSISTENT),
+                           ("kernels", myos.DECODE_KERNELS)):
+            try:
+                m.set_decode_mode(mode)
+            except myos.MyosError:
+                continue
+            m.cache_clear()
+            m.prefill(prompt)
+            m.decode_forced(ref["ids"])
+            g = m.logits().astype(np.float64)
+            rel[name] = float(np.max(np.abs(g - o_lg)) / np.max(np.abs(o_lg)))
+        m.set_decode_mode(myos.DECODE_AUTO)
+        parity = {"ids_equal_oracle_prefix": f"{agree}/{args.decode}",
+                  "first_divergence": first_div,
+                  "min_oracle_top2_gap": round(float(min(ref["gaps"])), 6),
+                  "teacher_forced_final_logits_max_rel_err_vs_oracle": rel}
 
     # the dominant kernel: the cooperative decode kernel (one launch runs all
     # decode steps of a greedy_decode call) or, on the per-kernel path, the
@@ -241,15 +387,19 @@ def main():
         launch_bytes = b_tok * args.decode
         launch_s = dd / args.steps * 1e-3
         achieved = launch_bytes / launch_s
-        traffic = None
+        traffic, tsrc = None, None
         t = tinfo.get("persistent_launch")
         if t and t.get("decode_steps") == args.decode and t.get("prompt_ids") == args.prompt:
-            traffic = t["traffic_bytes"]
+            traffic, tsrc = t["traffic_bytes"], t["source"]
         roofline = {"bound": "hbm",
                     "kernel": f"decode_persistent_kernel (one launch: {args.decode} greedy "
                               f"decode steps)",
                     "achieved": round(achieved / 1e9, 1), "peak": HBM_PEAK / 1e9,
                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK, 4), "traffic": traffic,
+                    "traffic_source": tsrc and f"{tsrc}: rocprofv3 --pmc FETCH_SIZE and "
+                                               f"WRITE_SIZE of the same launch, scaled by a "
+                                               f"copy-kernel calibration (not measured in "
+                                               f"this run)",
                     "algorithmic_bytes": int(launch_bytes),
                     "avg_launch_ms": round(dd / args.steps, 3)}
     else:
@@ -260,6 +410,7 @@ def main():
                     "achieved": round(achieved / 1e9, 1), "peak": HBM_PEAK / 1e9,
                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK, 4),
                     "traffic": tinfo.get("traffic_bytes_per_launch", {}).get("gate_up_swiglu"),
+                    "traffic_source": tinfo.get("source"),
                     "algorithmic_bytes": dom["bytes"]}
     m.close()
 
@@ -269,17 +420,20 @@ def main():
                                              for n, v in micro.items()))
 
     cpu = None
-    if not args.no_cpu_baseline:
-        n = args.cpu_decode_steps
-        cores, res, match = cpu_baseline(path, shape, prompt, n, ids0)
-        r = res[cores]
-        cpu = {"value": round(n / r["decode_s"], 3), "unit": "tok/s", "cores": cores,
+    if cpu_res:
+        cores = host_cores()
+        r = cpu_res[cores]
+        cpu = {"value": round(n_cpu / r["decode_s"], 3), "unit": "tok/s", "cores": cores,
                "kind": "port",
-               "sample": f"same weights file and 128 prompt ids: prefill 128 then {n} greedy "
-                         f"decode steps on the C oracle (AVX2 GEMV, {cores} threads)",
+               "sample": f"same weights file and {args.prompt} prompt ids: prefill then {n_cpu} "
+                         f"greedy decode steps on the C oracle (AVX2 32-row GEMV over a "
+                         f"row-span thread pool), median of {args.cpu_repeats} runs after a "
+                         f"warm-up, at {cores} threads (host nproc {host_nproc()}; a GPU box "
+                         f"allots 16 cores per GPU) and at 8 threads",
+               "host_nproc": host_nproc(),
                "prefill_tok_s": round(len(prompt) / r["prefill_s"], 2),
-               "threads8_decode_tok_s": round(n / res[8]["decode_s"], 3) if 8 in res else None,
-               "gpu_ids_equal_oracle_first_n": f"{match}/{n}"}
+               "threads8_decode_tok_s": round(n_cpu / cpu_res[8]["decode_s"], 3) if 8 in cpu_res else None,
+               "threads8_prefill_tok_s": round(len(prompt) / cpu_res[8]["prefill_s"], 2) if 8 in cpu_res else None}
 
     line = {
         "metric": METRIC, "value": round(decode_tok_s, 2), "unit": "tok/s", "n_gpus": 1,
@@ -292,7 +446,12 @@ def main():
         "config": {"workload": f"{'Qwen2.5-7B' if is7b else 'Qwen2.5-1.5B'}-shape S1: {args.prompt} prompt ids prefilled + "
                                f"{args.decode} greedy decode steps, batch 1",
                    "prompt_ids": args.prompt, "decode_steps": args.decode, "batch": 1,
-                   "max_seq": max_seq, "kv_cache": args.kv, "accumulate": "f32",
+                   "max_seq": max_seq, "kv_cache": args.kv,
+                   "accumulate": "f32 accumulate over bf16 weights; activations enter the "
+                                 "products split into bf16 hi + lo terms (16 significant bits): "
+                                 "the MFMA prefill, and the cooperative decode kernel's "
+                                 "gate/up, down and head (v_dot2); its QKV, o and attention, "
+                                 "and the per-kernel decode path, keep f32 activations",
                    "decode_path": path_name, "graph": not args.no_graph,
                    "parallelism": "single GPU"},
         "prefill_tok_s": round(prefill_tok_s, 1),
@@ -301,7 +460,9 @@ def main():
         "decode_roofline": {"bytes_per_token": int(b_tok), "achieved_GBps":
                             round(decode_tok_s * b_tok / 1e9, 1), "peak_GBps": HBM_PEAK / 1e9,
                             "frac": round(decode_frac, 4)},
-        "roofline": roofline, "per_kernel_path": kernels, "gemv_microbench": micro,
+        "prefill_roofline": pf_roof,
+        "roofline": roofline, "parity": parity, "arena": arena,
+        "per_kernel_path": kernels, "gemv_microbench": micro,
         "t_load_s": round(t_load, 2),
         "cpu_baseline": cpu,
     }

@@ -238,6 +238,11 @@ double myos_kernel_bytes(const myos_model *m, int which);
 int myos_write_random_qwen25(const char *path, const myos_block_shape *shape, uint64_t seed,
                              float std_dev, int threads);
 
+/* SHA-256 of a file as 64 lowercase hex digits + NUL in out_hex[65], for the
+ * run fingerprint's model_sha256 field (fingerprint.rs:63-206, which the
+ * reference leaves null). Host only. MYOS_E_IO if the file cannot be read. */
+int myos_sha256_file(const char *path, char *out_hex);
+
 #ifdef __cplusplus
 }
 #endif

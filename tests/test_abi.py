@@ -214,3 +214,18 @@ def test_random_writer_matches_restatement(tmp_path):
     # sample statistics of a larger tensor: N(0, 0.02)
     w = oracle.bf16_to_f32(t["model.layers.0.mlp.gate_proj.weight"]).astype(np.float64)
     assert abs(w.mean()) < 0.01 and 0.012 < w.std() < 0.028
+
+
+def test_sha256_file_matches_hashlib(tmp_path):
+    # myos_sha256_file (the fingerprint's model_sha256) against hashlib at the
+    # padding edges (55 / 56 / 64 bytes) and across the 1 MiB read buffer
+    import hashlib
+    rng = np.random.default_rng(1)
+    for n in (0, 3, 55, 56, 63, 64, 65, (1 << 20) - 1, 1 << 20, (1 << 20) + 57):
+        data = rng.integers(0, 256, n, dtype=np.uint8).tobytes()
+        p = tmp_path / f"f{n}.bin"
+        p.write_bytes(data)
+        assert myos.sha256_file(str(p)) == hashlib.sha256(data).hexdigest(), n
+    with pytest.raises(myos.MyosError) as e:
+        myos.sha256_file(str(tmp_path / "missing.bin"))
+    assert e.value.kind == "Io"

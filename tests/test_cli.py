@@ -5,6 +5,7 @@ meter.rs:183-232) over the device library.
 Argument handling runs on the CPU; decodes are marked gpu and checked
 against the oracle.
 """
+import hashlib
 import importlib
 import json
 import os
@@ -47,7 +48,17 @@ def built():
     (["--block-fixture", "--weights", "w", "--prompt-ids", "p"],
      "--prompt-ids cannot be combined with --block-fixture"),
     (["--bogus"], "unknown argument `--bogus`"),
-    (["--arena-s1"], "not part of the device build"),
+    (["--cost-card", "c.md"], "the llama.cpp cost card is not part of the device build"),
+    (["--arena-s1"], "--arena-s1 needs --weights"),
+    (["--arena-s1", "--weights", "w"], "--arena-s1 needs --prompt-ids"),
+    (["--arena-s1", "--weights", "w", "--prompt-ids", "p"], "--arena-s1 needs --ref-ids"),
+    (["--arena-s1", "--block-fixture"], "--arena-s1 cannot be combined with --block-fixture"),
+    (["--arena-s1", "--arena-s1"], "--arena-s1 was given more than once"),
+    (["--warmup", "1"], "--warmup and --repeats need --arena-s1"),
+    (["--repeats", "0"], "--repeats needs a positive integer, got `0`"),
+    (["--warmup=x"], "--warmup needs a non-negative integer, got `x`"),
+    (["--teacher-forced", "--block-fixture"], "--teacher-forced needs --ref-ids"),
+    (["--gaps", "--gaps"], "--gaps was given more than once"),
     (["--kv", "f16"], "--kv needs f32 or bf16"),
 ])
 def test_argument_errors(args, msg):
@@ -80,12 +91,21 @@ def test_block_fixture_cli(tmp_path):
 
 
 @pytest.fixture(scope="module")
-def qwen15(tmp_path_factory):
-    path = os.environ.get("MYOS_TEST_WEIGHTS_1_5B")
-    if not path:
-        path = str(tmp_path_factory.mktemp("w") / "qwen25_1_5b_seed0.safetensors")
-        myos.write_random_qwen25(path, myos.preset(myos.SHAPE_QWEN25_1_5B), seed=0, std=0.02)
-    return path
+def qwen15(qwen15_path):
+    return qwen15_path
+
+
+def _oracle_ids(path, prompt, steps):
+    s = shape_dict(1536, 12, 2, 128, 8960, 151936, 28, 1e-6)
+    o = oracle.Model(s, oracle.load_safetensors_bits(path), len(prompt) + steps, threads=16)
+    assert o.prefill(prompt) == 0
+    ids, gaps = [], []
+    for _ in range(steps):
+        lg = o.logits()
+        ids.append(int(oracle.greedy_token(lg)))
+        gaps.append(top2_gap(lg))
+        assert o.forward_token(ids[-1], o.cache_len()) == 0
+    return ids, gaps
 
 
 @pytest.mark.gpu
@@ -94,15 +114,7 @@ def test_weights_cli_qwen15(tmp_path, qwen15):
     preset: ids equal the oracle's greedy ids, and the three files carry the
     reference's fields plus the device ones."""
     prompt = [int(v) for v in np.random.default_rng(7).integers(0, 151936, 16)]
-    s = shape_dict(1536, 12, 2, 128, 8960, 151936, 28, 1e-6)
-    o = oracle.Model(s, oracle.load_safetensors_bits(qwen15), len(prompt) + 4, threads=16)
-    assert o.prefill(prompt) == 0
-    ids, gaps = [], []
-    for _ in range(4):
-        lg = o.logits()
-        ids.append(int(oracle.greedy_token(lg)))
-        gaps.append(top2_gap(lg))
-        assert o.forward_token(ids[-1], o.cache_len()) == 0
+    ids, gaps = _oracle_ids(qwen15, prompt, 4)
     if min(gaps) <= GAP:
         pytest.skip(f"the oracle has a near-tie (top-2 gap {min(gaps):.2e}): ids may differ")
     (tmp_path / "p.txt").write_text(" ".join(map(str, prompt)) + "\n")
@@ -123,3 +135,78 @@ def test_weights_cli_qwen15(tmp_path, qwen15):
               "L_TPOT_ms", "T_e2e_tok_s", "device_decode_ms", "device_prefill_ms"):
         assert isinstance(m[k], float) and m[k] > 0, k
     assert m["correct"] is True and m["n_gen"] == 4
+    # device fields
+    assert m["arch"] == "gfx950" and m["hbm_peak_GBps"] == 8000.0
+    assert 0 < m["roofline_frac"] < 1 and m["achieved_GBps"] > 0
+    assert m["decode_bytes_per_token"] > 3.087e9
+    assert m["verify_mode"] is None and m["top2_gap_per_step"] is None
+    assert m["M_peak_KiB"] > 0 and m["M_hwm_KiB"] >= m["M_peak_KiB"]
+    h = hashlib.sha256()
+    with open(qwen15, "rb") as fh:
+        for blk in iter(lambda: fh.read(1 << 24), b""):
+            h.update(blk)
+    assert m["model_sha256"] == f["model_sha256"] == h.hexdigest()
+
+
+@pytest.mark.gpu
+def test_cli_gaps_and_teacher_forced(tmp_path, qwen15):
+    """--gaps re-runs the decode one step per call and exports each step's
+    top-1 / top-2 gap; --teacher-forced feeds the reference ids and reports
+    agreement. Reference ids = the oracle's greedy ids; the last one is
+    changed, so the forced pass must still agree on every step (the id a
+    step is fed does not change the logits it starts from)."""
+    prompt = [int(v) for v in np.random.default_rng(9).integers(0, 151936, 12)]
+    ids, gaps = _oracle_ids(qwen15, prompt, 6)
+    if min(gaps) <= GAP:
+        pytest.skip(f"the oracle has a near-tie (top-2 gap {min(gaps):.2e}): ids may differ")
+    (tmp_path / "p.txt").write_text(" ".join(map(str, prompt)) + "\n")
+    (tmp_path / "r.txt").write_text(" ".join(map(str, ids)) + "\n")
+    r = run("--weights", qwen15, "--prompt-ids", str(tmp_path / "p.txt"), "--steps", "6",
+            "--ref-ids", str(tmp_path / "r.txt"), "--fingerprint-dir", str(tmp_path / "g"),
+            "--gaps")
+    assert r.returncode == 0, r.stderr
+    m = json.loads((tmp_path / "g" / "metrics.json").read_text())
+    assert m["verify_mode"] == "greedy" and m["verify_ids"] == ids and m["verify_agree"] == 6
+    assert len(m["top2_gap_per_step"]) == 6
+    for got, want in zip(m["top2_gap_per_step"], gaps):
+        assert abs(got - want) <= 1e-2 * max(1.0, want), (got, want)
+    bent = ids[:-1] + [(ids[-1] + 1) % 151936]
+    (tmp_path / "b.txt").write_text(" ".join(map(str, bent)) + "\n")
+    r = run("--weights", qwen15, "--prompt-ids", str(tmp_path / "p.txt"), "--steps", "6",
+            "--ref-ids", str(tmp_path / "b.txt"), "--fingerprint-dir", str(tmp_path / "t"),
+            "--teacher-forced")
+    assert r.returncode == 0, r.stderr
+    assert "CORRECT: FAIL first_diff@5" in r.stdout
+    assert "TEACHER-FORCED: 5/6 first_diff@5" in r.stdout, r.stdout
+    m = json.loads((tmp_path / "t" / "metrics.json").read_text())
+    assert m["verify_mode"] == "teacher-forced" and m["verify_ids"][:5] == bent[:5]
+
+
+@pytest.mark.gpu
+def test_cli_arena_w1_r2(tmp_path, qwen15):
+    """--arena-s1 (arena.rs:41-260): one warm-up and two scored fresh
+    processes, medians, DET across the scored runs, CORRECT against the
+    oracle's ids."""
+    prompt = [int(v) for v in np.random.default_rng(5).integers(0, 151936, 8)]
+    ids, gaps = _oracle_ids(qwen15, prompt, 5)
+    if min(gaps) <= GAP:
+        pytest.skip(f"the oracle has a near-tie (top-2 gap {min(gaps):.2e}): ids may differ")
+    (tmp_path / "p.txt").write_text(" ".join(map(str, prompt)) + "\n")
+    (tmp_path / "r.txt").write_text(" ".join(map(str, ids)) + "\n")
+    out = tmp_path / "arena"
+    r = run("--arena-s1", "--weights", qwen15, "--prompt-ids", str(tmp_path / "p.txt"),
+            "--ref-ids", str(tmp_path / "r.txt"), "--steps", "5", "--warmup", "1",
+            "--repeats", "2", "--fingerprint-dir", str(out))
+    assert r.returncode == 0, (r.stdout, r.stderr)
+    assert "ARENA S1 threads=8 W=1 R=2 CORRECT=PASS DET=PASS" in r.stdout, r.stdout
+    assert "=== WARM 1/1 ===" in r.stderr and "=== SCORE 2/2 ===" in r.stderr
+    agg = json.loads((out / "metrics.json").read_text())
+    assert agg["W"] == 1 and agg["R"] == 2 and agg["det"] == "PASS" and agg["CORRECT"] == "PASS"
+    assert len(agg["per_run_scored"]) == 2 and len(agg["per_run_warmup_discarded"]) == 1
+    runs = [json.loads((out / f"score-{i}" / "metrics.json").read_text()) for i in (1, 2)]
+    tds = sorted(x["T_decode_tok_s"] for x in runs)
+    assert abs(agg["median"]["T_decode_tok_s"] - (tds[0] + tds[1]) / 2) < 1e-3 * tds[1]
+    ev = json.loads((out / "det_evidence.json").read_text())
+    assert ev["scored_ids"] == [ids, ids] and ev["ref_ids"] == ids
+    assert [int(v) for v in (out / "token_ids.txt").read_text().split()] == ids
+    assert (out / "warm-1" / "stdout.txt").exists()
