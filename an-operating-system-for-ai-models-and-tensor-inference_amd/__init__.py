@@ -26,12 +26,13 @@ INCLUDE = os.path.join(os.path.dirname(PKG_DIR), "include", "myos_hip.h")
 
 OK, E_SHAPE, E_TOKEN, E_ROW_OOB, E_POSITION, E_KV_FULL, E_KV_RANGE = range(7)
 E_W_MISSING, E_W_DTYPE, E_W_SHAPE, E_W_LENGTH, E_IO, E_PARSE, E_HIP, E_ARG = range(7, 15)
+E_SCRATCH = 15
 
 KIND = {
     E_SHAPE: "Shape", E_TOKEN: "TokenOutOfBounds", E_ROW_OOB: "RowOutOfBounds",
     E_POSITION: "Position", E_KV_FULL: "Full", E_KV_RANGE: "Range", E_W_MISSING: "Missing",
     E_W_DTYPE: "DType", E_W_SHAPE: "WeightShape", E_W_LENGTH: "Length", E_IO: "Io",
-    E_PARSE: "Parse", E_HIP: "Hip", E_ARG: "Arg",
+    E_PARSE: "Parse", E_HIP: "Hip", E_ARG: "Arg", E_SCRATCH: "Scratch",
 }
 
 KV_F32, KV_BF16 = 0, 1
@@ -65,6 +66,9 @@ EXPORTS = {
     "myos_build_info": ([], C.c_char_p),
     "myos_gemv_bf16": ([P, SZ, P, SZ, P, SZ, SZ, SZ, P], I32),
     "myos_gemm_bf16": ([P, SZ, P, SZ, P, SZ, SZ, SZ, SZ, P], I32),
+    "myos_gemm_bf16_noalloc": ([P, SZ, P, SZ, P, SZ, SZ, SZ, SZ, P], I32),
+    "myos_gemm_bf16_noalloc_scratch": ([SZ, SZ, SZ], SZ),
+    "myos_gemm_bf16_noalloc_max_scratch": ([], SZ),
     "myos_add_bf16_bias": ([P, SZ, P, SZ, P], I32),
     "myos_embed_gather_bf16": ([P, SZ, P, SZ, SZ, SZ, U32, P], I32),
     "myos_rmsnorm_bf16_weight": ([P, SZ, P, SZ, P, SZ, F32, P], I32),
@@ -201,6 +205,16 @@ def gemm_bf16(y, w, x, batch, m, k, stream=None):
     xp, xn = _f32(x, "x")
     _check(lib().myos_gemm_bf16(yp, yn, wp, wn, xp, xn, batch, m, k, _stream(stream)),
            "gemm_bf16")
+
+
+def gemm_bf16_noalloc(y, w, x, batch, m, k, stream=None):
+    """gemm_bf16 with its scratch in the library's static device array (no
+    allocation); Scratch error past myos_gemm_bf16_noalloc_max_scratch()."""
+    yp, yn = _f32(y, "y")
+    wp, wn = _w16(w, "w")
+    xp, xn = _f32(x, "x")
+    _check(lib().myos_gemm_bf16_noalloc(yp, yn, wp, wn, xp, xn, batch, m, k, _stream(stream)),
+           "gemm_bf16_noalloc")
 
 
 def add_bf16_bias(y, bias, stream=None):

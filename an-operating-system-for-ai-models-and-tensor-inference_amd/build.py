@@ -18,7 +18,7 @@ LIB = os.path.join(OUT, "libmyos_hip.so")
 ARCH = os.environ.get("MYOS_OFFLOAD_ARCH", "gfx950")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
-SOURCES = ["myos_kernels.hip", "myos_persistent.hip", "myos_ops.cpp", "myos_model.cpp",
+SOURCES = ["myos_kernels.hip", "myos_persistent.hip", "myos_noalloc.hip", "myos_ops.cpp", "myos_model.cpp",
            "myos_safetensors.cpp",
            "myos_gen.cpp", "myos_sha256.cpp"]
 CLI_SOURCES = ["myos_cli.cpp", "myos_arena.cpp"]

@@ -41,6 +41,7 @@ const char *myos_strerror(int status) {
     case MYOS_E_PARSE: return "weight buffer could not be parsed";
     case MYOS_E_HIP: return "HIP runtime error";
     case MYOS_E_ARG: return "invalid argument";
+    case MYOS_E_SCRATCH: return "call needs more than the static scratch of the no-allocation entry point";
     default: return "unknown status";
   }
 }

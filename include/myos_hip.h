@@ -45,6 +45,8 @@ enum {
   MYOS_E_PARSE = 12,       /* WeightError::Parse / Duplicate / EmptyName / UnsupportedDType */
   MYOS_E_HIP = 13,         /* a HIP runtime call failed (no reference counterpart) */
   MYOS_E_ARG = 14,         /* NULL handle or pointer, unknown enum value */
+  MYOS_E_SCRATCH = 15,     /* a no-allocation call needs more than its static scratch
+                              (no reference counterpart) */
 };
 
 typedef void *myos_stream_t; /* a hipStream_t */
@@ -72,6 +74,23 @@ int myos_gemv_bf16(float *y, size_t y_len, const uint16_t *w, size_t w_len, cons
  * bits. The reference's caller-provided scratch is internal here. */
 int myos_gemm_bf16(float *y, size_t y_len, const uint16_t *w, size_t w_len, const float *x,
                    size_t x_len, size_t batch, size_t m, size_t k, myos_stream_t stream);
+
+/* myos_gemm_bf16 without any allocation. No counterpart in the reference:
+ * this is for callers that cannot allocate device memory (code under stream
+ * capture, tight serving loops). Same arguments, checks, kernels and results
+ * (bit for bit) as myos_gemm_bf16, whose scratch (the bf16 hi / lo planes of
+ * X and the K-split partials) comes instead from one static device array of
+ * myos_gemm_bf16_noalloc_max_scratch() bytes (32 MiB) per GPU, held until
+ * the process ends. A call needing more (myos_gemm_bf16_noalloc_scratch)
+ * returns MYOS_E_SCRATCH before anything is launched. All calls on one GPU
+ * share that GPU's array: calls that overlap on one GPU race. */
+int myos_gemm_bf16_noalloc(float *y, size_t y_len, const uint16_t *w, size_t w_len,
+                           const float *x, size_t x_len, size_t batch, size_t m, size_t k,
+                           myos_stream_t stream);
+/* Scratch bytes a myos_gemm_bf16_noalloc call of this shape needs (0 when it
+ * launches nothing), and the static array's size. */
+size_t myos_gemm_bf16_noalloc_scratch(size_t batch, size_t m, size_t k);
+size_t myos_gemm_bf16_noalloc_max_scratch(void);
 
 /* add_bf16_bias, bf16.rs:147-158: y[i] += bf16(bias[i]); bias_len != y_len -> SHAPE. */
 int myos_add_bf16_bias(float *y, size_t y_len, const uint16_t *bias, size_t bias_len,
