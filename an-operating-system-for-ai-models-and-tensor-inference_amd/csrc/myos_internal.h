@@ -119,9 +119,16 @@ struct GemmArgs {
   size_t ws_cap;               // floats at ws
   int kps;                     // set by the launcher: K steps per split
 };
-// K splits launch_gemm uses for this shape (about one workgroup per CU), and
-// the partial-buffer floats they need (0 when one split)
-int gemm_splits(int M, int N, int K);
+// Launch plan of the pipelined MFMA GEMM: tile shape (cfg 0..3 = 128 x 32,
+// 64, 128, 256; -1 = the shape needs the fallback kernel) and K splits
+struct GemmPlan {
+  int cfg = -1;
+  int splits = 1;
+};
+GemmPlan pf_plan(int M, int N, int K);
+// force every later plan to (cfg, splits); cfg < 0 restores the planner
+void gemm_force_plan(int cfg, int splits);
+// the partial-buffer floats launch_gemm needs for this shape (0: one split)
 size_t gemm_ws_floats(int M, int N, int K);
 hipError_t launch_gemm(const GemmArgs &a, GemvEpi epi, hipStream_t s);
 // EPI_RESID GEMM (y += A W^T) followed by the RMSNorm of y with gains g into

@@ -11,6 +11,8 @@
 #include <math.h>
 #include <stdint.h>
 
+#include <algorithm>
+
 #include "myos_internal.h"
 
 namespace myos {
@@ -906,6 +908,206 @@ __global__ void __launch_bounds__(kBlock) gemm_mfma_kernel(GemmArgs a) {
   }
 }
 
+// ---- prefill GEMM with a two-stage LDS pipeline (K % 64 == 0) ---------------
+//
+// C[M,N] = (A_hi + A_lo)[M,K] . W[N,K]^T on v_mfma_f32_32x32x16_bf16. The
+// workgroup is WGM x WGN wavefronts; wave (wm, wn) owns a (32 MB) x (32 NB)
+// block of the (32 MB WGM) x (32 NB WGN) workgroup tile, MB x NB accumulators.
+// Per 64-wide K stage every thread loads its share of the A hi/lo and W rows
+// as 16-byte chunks (a wavefront load covers 8 rows x 128 B) into one of
+// three register sets, through buffer descriptors whose range ends at the
+// matrix, so rows past M or N read as zero; a set goes to one of two LDS
+// stages while the other stage is multiplied, one barrier per stage. Loads run
+// two stages ahead of their LDS store, and every stage issues its loads
+// unconditionally (a stage past the split reads out of range: zeros, no
+// traffic), so the compiler's wait before a store leaves the younger stages in
+// flight. An LDS row is the 128 B of one matrix row with chunk c at slot
+// c ^ (row & 7) ^ ((row >> 3) & 1): the 8 or 16 consecutive rows an MFMA
+// fragment read serves per LDS cycle (32 or 64 banks) hit distinct banks, and
+// so do the chunk stores. The next 16-wide K step's fragments are read from
+// LDS while the current step's MFMAs run.
+// LDS bytes per MFMA fall with MB and NB: (2 MB + NB) 1 KB fragments feed
+// 2 MB NB MFMAs (the hi and the lo term share each W fragment).
+template <int MB_, int NB_, int WGM_, int WGN_>
+struct PfCfg {
+  static constexpr int MB = MB_, NB = NB_, WGM = WGM_, WGN = WGN_;
+  static constexpr int NTH = 64 * WGM * WGN;
+  static constexpr int BM = 32 * MB * WGM, BN = 32 * NB * WGN;
+  static constexpr int ACH = BM * 8, WCH = BN * 8;  // 16-byte chunks per stage
+  static constexpr int ALD = (ACH + NTH - 1) / NTH, WLD = (WCH + NTH - 1) / NTH;
+  static constexpr int AL_OFF = ACH * 16, W_OFF = 2 * ACH * 16;
+  static constexpr int STAGE = (2 * ACH + WCH) * 16;
+  static constexpr int LDS = 2 * STAGE;
+  static constexpr int R = 3;  // register sets: loads run R - 1 stages ahead
+};
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t pf_rsrc(const uint16_t *base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, (int)bytes, 0x00020000);
+}
+
+template <class C, int EPI>
+__global__ void __launch_bounds__(C::NTH) gemm_pf_kernel(GemmArgs a) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t pf_sm[];
+  constexpr int R = C::R;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave % C::WGM, wn = wave / C::WGM;
+  const int n0 = blockIdx.x * C::BN, m0 = blockIdx.y * C::BM;
+  const int M = a.M, N = a.N, K = a.K;
+  const int nks = K >> 6, S = gridDim.z, z = blockIdx.z;
+  const int ks0 = (int)((long)z * nks / S), ks1 = (int)((long)(z + 1) * nks / S);
+  const int nst = ks1 - ks0;
+  // descriptors start at the tile's first row; rows past the matrix read 0
+  const __amdgpu_buffer_rsrc_t rah = pf_rsrc(a.a_hi + (size_t)m0 * K, (uint32_t)(M - m0) * K * 2);
+  const __amdgpu_buffer_rsrc_t ral = pf_rsrc(a.a_lo + (size_t)m0 * K, (uint32_t)(M - m0) * K * 2);
+  const __amdgpu_buffer_rsrc_t rw = pf_rsrc(a.w + (size_t)n0 * K, (uint32_t)(N - n0) * K * 2);
+
+  u32x4 ra[R][C::ALD], rl[R][C::ALD], rb[R][C::WLD];
+  // stage ks into register set `set`; a stage past the split sits at byte
+  // offset 2^31 of each row, beyond every descriptor's range (< 2^31 bytes)
+  auto gload = [&](int set, int ks) {
+    const uint32_t kb = ks < ks1 ? (uint32_t)ks * 128u : 0x80000000u;
+#pragma unroll
+    for (int i = 0; i < C::ALD; i++) {
+      const int q = tid + i * C::NTH;
+      if (C::ACH % C::NTH == 0 || q < C::ACH) {
+        const int off = (int)((uint32_t)((q >> 3) * K * 2) + kb + (uint32_t)((q & 7) << 4));
+        ra[set][i] = __builtin_amdgcn_raw_buffer_load_b128(rah, off, 0, 0);
+        rl[set][i] = __builtin_amdgcn_raw_buffer_load_b128(ral, off, 0, 0);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < C::WLD; i++) {
+      const int q = tid + i * C::NTH;
+      if (C::WCH % C::NTH == 0 || q < C::WCH) {
+        const int off = (int)((uint32_t)((q >> 3) * K * 2) + kb + (uint32_t)((q & 7) << 4));
+        rb[set][i] = __builtin_amdgcn_raw_buffer_load_b128(rw, off, 0, 0);
+      }
+    }
+  };
+  auto swrite = [&](int set, int st) {
+    uint8_t *base = pf_sm + st * C::STAGE;
+#pragma unroll
+    for (int i = 0; i < C::ALD; i++) {
+      const int q = tid + i * C::NTH;
+      if (C::ACH % C::NTH == 0 || q < C::ACH) {
+        const int r = q >> 3, slot = ((q & 7) ^ (r & 7) ^ ((r >> 3) & 1)) << 4;
+        *(u32x4 *)(base + r * 128 + slot) = ra[set][i];
+        *(u32x4 *)(base + C::AL_OFF + r * 128 + slot) = rl[set][i];
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < C::WLD; i++) {
+      const int q = tid + i * C::NTH;
+      if (C::WCH % C::NTH == 0 || q < C::WCH) {
+        const int r = q >> 3, slot = ((q & 7) ^ (r & 7) ^ ((r >> 3) & 1)) << 4;
+        *(u32x4 *)(base + C::W_OFF + r * 128 + slot) = rb[set][i];
+      }
+    }
+  };
+
+  f32x16 acc[C::MB][C::NB];
+#pragma unroll
+  for (int i = 0; i < C::MB; i++)
+#pragma unroll
+    for (int j = 0; j < C::NB; j++)
+#pragma unroll
+      for (int e = 0; e < 16; e++) acc[i][j][e] = 0.f;
+
+  const int arow = (wm * C::MB * 32 + (lane & 31)) * 128;
+  const int wrow = (wn * C::NB * 32 + (lane & 31)) * 128;
+  // the 64-wide stage in LDS stage `st`: 4 K steps of 16, each step's
+  // fragments read while the previous step's MFMAs run
+  auto mult = [&](int st) {
+    const uint8_t *base = pf_sm + st * C::STAGE;
+    bf16x8 fh[2][C::MB], fl[2][C::MB], fw[2][C::NB];
+    auto ldfrag = [&](int buf, int ks) {
+      const int swz = ((2 * ks + (lane >> 5)) ^ (lane & 7) ^ ((lane >> 3) & 1)) << 4;
+#pragma unroll
+      for (int i = 0; i < C::MB; i++) {
+        fh[buf][i] = __builtin_bit_cast(bf16x8, *(const u32x4 *)(base + arow + i * 4096 + swz));
+        fl[buf][i] = __builtin_bit_cast(bf16x8, *(const u32x4 *)(base + C::AL_OFF + arow + i * 4096 + swz));
+      }
+#pragma unroll
+      for (int j = 0; j < C::NB; j++)
+        fw[buf][j] = __builtin_bit_cast(bf16x8, *(const u32x4 *)(base + C::W_OFF + wrow + j * 4096 + swz));
+    };
+    ldfrag(0, 0);
+#pragma unroll
+    for (int ks = 0; ks < 4; ks++) {
+      const int b = ks & 1;
+      if (ks + 1 < 4) ldfrag(b ^ 1, ks + 1);
+#pragma unroll
+      for (int i = 0; i < C::MB; i++)
+#pragma unroll
+        for (int j = 0; j < C::NB; j++)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fh[b][i], fw[b][j], acc[i][j], 0, 0, 0);
+#pragma unroll
+      for (int i = 0; i < C::MB; i++)
+#pragma unroll
+        for (int j = 0; j < C::NB; j++)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fl[b][i], fw[b][j], acc[i][j], 0, 0, 0);
+    }
+  };
+
+  // stage s lives in register set s % R and LDS stage s & 1
+  if (nst > 0) {
+    gload(0, ks0);
+    swrite(0, 0);
+#pragma unroll
+    for (int s = 1; s < R; s++) gload(s, ks0 + s);
+  }
+  __syncthreads();
+  const int nfull = nst / R * R;
+  for (int it0 = 0; it0 < nfull; it0 += R) {
+#pragma unroll
+    for (int u = 0; u < R; u++) {
+      const int it = it0 + u;
+      swrite((u + 1) % R, (it & 1) ^ 1);
+      gload(u, ks0 + it + R);
+      mult(it & 1);
+      __syncthreads();
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < R; u++) {
+    const int it = nfull + u;
+    if (it < nst) {
+      swrite((u + 1) % R, (it & 1) ^ 1);
+      mult(it & 1);
+      __syncthreads();
+    }
+  }
+
+  // the accumulator tile goes through LDS (free after the last stage's
+  // barrier), then each thread takes elements tid, tid + NTH, ... in row-major
+  // order: coalesced stores, and the epilogue's partner column (col ^ 1) is a
+  // plain LDS read
+  static_assert(C::BM * C::BN * 4 <= C::LDS, "accumulator tile exceeds the LDS stages");
+  float *cs = (float *)pf_sm;
+#pragma unroll
+  for (int i = 0; i < C::MB; i++)
+#pragma unroll
+    for (int j = 0; j < C::NB; j++)
+#pragma unroll
+      for (int e = 0; e < 16; e++) {
+        const int tr = wm * C::MB * 32 + i * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
+        const int tc = wn * C::NB * 32 + j * 32 + (lane & 31);
+        cs[tr * C::BN + tc] = acc[i][j][e];
+      }
+  __syncthreads();
+  const bool split = S > 1;
+  float *ws = a.ws + (size_t)z * M * N;
+  for (int idx = tid; idx < C::BM * C::BN; idx += C::NTH) {
+    const int tr = idx / C::BN, tc = idx % C::BN;
+    const int row = m0 + tr, col = n0 + tc;
+    if (row < M && col < N) {
+      const float c = cs[idx];
+      if (split) ws[(size_t)row * N + col] = c;
+      else gemm_store<EPI>(a, row, col, c, cs[idx ^ 1]);
+    }
+  }
+}
+
 // EPI_RESID's K splits fused with the RMSNorm that reads the result: row r of
 // y += (the splits of row r, added in split order), then the normalised row
 // (gains g) as bf16 hi/lo planes, as rmsnorm_rows_split_kernel writes them.
@@ -1413,7 +1615,73 @@ hipError_t launch_split_rows(const float *X, size_t n, uint16_t *hi, uint16_t *l
   return hipGetLastError();
 }
 
-int gemm_splits(int M, int N, int K) {
+// ---- GEMM launch plans ------------------------------------------------------
+// The pipelined kernel's tile shapes (M x N): 128 x 32, 128 x 64, 128 x 128,
+// 128 x 256. Wider tiles read fewer A bytes per weight byte (the A tile is
+// re-read by every N tile) and fewer LDS bytes per MFMA; narrower ones give
+// more workgroups when N is small.
+using PfT32 = PfCfg<1, 1, 4, 1>;
+using PfT64 = PfCfg<1, 2, 4, 1>;
+using PfT128 = PfCfg<2, 2, 2, 2>;
+using PfT256 = PfCfg<2, 4, 2, 2>;
+constexpr int kPfCfgs = 4;
+constexpr int kPfBN[kPfCfgs] = {PfT32::BN, PfT64::BN, PfT128::BN, PfT256::BN};
+constexpr int kCUs = 256;
+
+int g_force_cfg = -1, g_force_splits = 0;
+
+// Tile shape and K splits for the pipelined kernel, from a cost model fitted
+// to measurements of this kernel on MI355X over the prefill shapes (1.5B and
+// 7B projections at 128 and 2048 rows). A workgroup is bound by what its CU
+// can pull from L2: about 64 outstanding 128-byte L2 requests at ~520 cycles
+// each, 14 B/clk, so a 64-wide K stage costs (A hi/lo 128 x 256 B + W
+// BN x 128 B) / 14 clocks; workgroups beyond one per CU run in further
+// rounds; K splits add their f32 partials written and read back at ~2 TB/s
+// and a reduction launch. Wider tiles re-read the A tile fewer times per
+// weight byte; split K fills the CUs when N has few tiles.
+GemmPlan pf_plan(int M, int N, int K) {
+  GemmPlan best;
+  if (K <= 0 || (K & 63) || M <= 0 || N <= 0) return best;
+  if (g_force_cfg >= 0) {
+    best.cfg = g_force_cfg;
+    best.splits = g_force_splits > 0 ? std::min(g_force_splits, K >> 6) : 1;
+    return best;
+  }
+  const int nks = K >> 6;
+  const long mt = (M + 127) / 128;
+  double best_t = 1e30;
+  for (int c = 0; c < kPfCfgs; c++) {
+    const long tiles = mt * ((N + kPfBN[c] - 1) / kPfBN[c]);
+    const double stage = (32768.0 + 128.0 * kPfBN[c]) / 14.0;  // clocks per K stage
+    for (int sp = 1; sp <= std::min(nks, 64); sp++) {
+      const long rounds = (tiles * sp + kCUs - 1) / kCUs;
+      const int kst = (nks + sp - 1) / sp;
+      double t = rounds * (kst * stage + 1500.0) / 2400.0;  // us at 2.4 GHz
+      if (sp > 1) t += 2.0 * sp * (double)M * N * 4.0 / 2.0e6 + 1.0;
+      if (t < best_t - 1e-9) {
+        best_t = t;
+        best.cfg = c;
+        best.splits = sp;
+      }
+    }
+  }
+  return best;
+}
+
+void gemm_force_plan(int cfg, int splits) {
+  g_force_cfg = cfg;
+  g_force_splits = splits;
+}
+
+// the pipelined kernel takes the shape: K stages of 64, 16-byte aligned
+// operands, 32-bit buffer ranges
+static bool pf_ok(const GemmArgs &a) {
+  return a.K > 0 && (a.K & 63) == 0 && a.M > 0 && a.N > 0 &&
+         (((uintptr_t)a.a_hi | (uintptr_t)a.a_lo | (uintptr_t)a.w) & 15) == 0 &&
+         (size_t)a.M * a.K * 2 < (1ull << 31) && (size_t)a.N * a.K * 2 < (1ull << 31);
+}
+
+int gemm_splits_old(int M, int N, int K) {
   const int tiles = (int)(nblk((size_t)N, GBN) * nblk((size_t)M, GBM));
   const int ksteps = (K + GBK - 1) / GBK;
   // about two workgroups per CU, so one's operand loads overlap the other's
@@ -1428,36 +1696,82 @@ int gemm_splits(int M, int N, int K) {
 }
 
 size_t gemm_ws_floats(int M, int N, int K) {
-  const int sp = gemm_splits(M, N, K);
+  const GemmPlan p = pf_plan(M, N, K);
+  const int sp = std::max(p.cfg >= 0 ? p.splits : 1, gemm_splits_old(M, N, K));
   return sp > 1 ? (size_t)sp * M * N : 0;
 }
 
-// the launch shape of a GEMM: K splits (1 when the partial buffer is short)
-// and K steps per split in a.kps
-static int gemm_plan(GemmArgs &a) {
+// the fallback kernel's launch shape: K splits (1 when the partial buffer is
+// short) and K steps per split in a.kps
+static int gemm_plan_old(GemmArgs &a) {
   const int ksteps = (a.K + GBK - 1) / GBK;
-  int splits = gemm_splits(a.M, a.N, a.K);
+  int splits = gemm_splits_old(a.M, a.N, a.K);
   if (!a.ws || a.ws_cap < (size_t)splits * a.M * a.N) splits = 1;  // no room for partials
   a.kps = (ksteps + splits - 1) / splits;
   if (a.kps < 1) a.kps = 1;
   return splits;
 }
 
+template <class C, int EPI>
+static hipError_t go_pf(const GemmArgs &a, int splits, hipStream_t s) {
+  static bool attr_done = false;
+  const void *fn = (const void *)gemm_pf_kernel<C, EPI>;
+  if (!attr_done) {
+    hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS);
+    if (e != hipSuccess) return e;
+    attr_done = true;
+  }
+  dim3 grid(nblk((size_t)a.N, C::BN), nblk((size_t)a.M, C::BM), splits);
+  GemmArgs args = a;
+  void *params[] = {&args};
+  return hipLaunchKernel(fn, grid, dim3(C::NTH), params, C::LDS, s);
+}
+
+template <int EPI>
+static hipError_t go_pf_cfg(const GemmArgs &a, int cfg, int splits, hipStream_t s) {
+  switch (cfg) {
+    case 0: return go_pf<PfT32, EPI>(a, splits, s);
+    case 1: return go_pf<PfT64, EPI>(a, splits, s);
+    case 2: return go_pf<PfT128, EPI>(a, splits, s);
+    case 3: return go_pf<PfT256, EPI>(a, splits, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+// Launch the GEMM (partials into a.ws when split) with epilogue EPI, or with
+// EPI_STORE into the partials; returns the split count used in *splits_out.
+template <int EPI>
+static hipError_t gemm_main(GemmArgs &a, hipStream_t s, int *splits_out) {
+  const GemmPlan p = pf_plan(a.M, a.N, a.K);
+  if (p.cfg >= 0 && p.cfg < kPfCfgs && pf_ok(a) &&
+      (p.splits == 1 || (a.ws && a.ws_cap >= (size_t)p.splits * a.M * a.N))) {
+    *splits_out = p.splits;
+    return go_pf_cfg<EPI>(a, p.cfg, p.splits, s);
+  }
+  const int splits = gemm_plan_old(a);
+  *splits_out = splits;
+  dim3 grid(nblk((size_t)a.N, GBN), nblk((size_t)a.M, GBM), splits);
+  hipLaunchKernelGGL(gemm_mfma_kernel<EPI>, grid, dim3(kBlock), 0, s, a);
+  return hipGetLastError();
+}
+
 hipError_t launch_gemm_resid_norm(const GemmArgs &args, const uint16_t *g, float eps,
                                   uint16_t *hi, uint16_t *lo, hipStream_t s) {
   if (args.M <= 0 || args.N <= 0) return hipSuccess;
   GemmArgs a = args;
-  const int splits = gemm_plan(a);
   const int n4 = a.N >> 2;
-  const bool fused = splits > 1 && (a.N & 3) == 0 && n4 <= 4 * kBlock &&
-                     (((uintptr_t)a.ws | (uintptr_t)a.y) & 15) == 0;
-  if (!fused) {
-    hipError_t e = launch_gemm(args, EPI_RESID, s);
-    if (e != hipSuccess) return e;
+  const bool can_fuse = (a.N & 3) == 0 && n4 <= 4 * kBlock &&
+                        (((uintptr_t)a.ws | (uintptr_t)a.y) & 15) == 0;
+  int splits = 1;
+  hipError_t e = gemm_main<EPI_RESID>(a, s, &splits);
+  if (e != hipSuccess) return e;
+  if (splits == 1 || !can_fuse) {
+    if (splits > 1) {  // plain split reduction into y, then the norm
+      const unsigned rgrid = nblk((size_t)a.M * ((a.N + 1) >> 1), kBlock);
+      hipLaunchKernelGGL(gemm_reduce_kernel<EPI_RESID>, dim3(rgrid), dim3(kBlock), 0, s, a, splits);
+    }
     return launch_rmsnorm_rows_split(a.y, g, eps, a.M, a.N, hi, lo, s);
   }
-  dim3 grid(nblk((size_t)a.N, GBN), nblk((size_t)a.M, GBM), splits);
-  hipLaunchKernelGGL(gemm_mfma_kernel<EPI_RESID>, grid, dim3(kBlock), 0, s, a);
   if (n4 <= kBlock)
     hipLaunchKernelGGL(gemm_resid_norm_kernel<1>, dim3(a.M), dim3(kBlock), 0, s, a, splits, g, eps, hi, lo);
   else if (n4 <= 2 * kBlock)
@@ -1467,32 +1781,32 @@ hipError_t launch_gemm_resid_norm(const GemmArgs &args, const uint16_t *g, float
   return hipGetLastError();
 }
 
-hipError_t launch_gemm(const GemmArgs &args, GemvEpi epi, hipStream_t s) {
-  if (args.M <= 0 || args.N <= 0) return hipSuccess;
+template <int EPI>
+static hipError_t launch_gemm_epi(const GemmArgs &args, hipStream_t s) {
   GemmArgs a = args;
-  const int splits = gemm_plan(a);
-  dim3 grid(nblk((size_t)a.N, GBN), nblk((size_t)a.M, GBM), splits);
-  const unsigned rgrid = nblk((size_t)a.M * ((a.N + 1) >> 1), kBlock);
+  int splits = 1;
+  hipError_t e = gemm_main<EPI>(a, s, &splits);
+  if (e != hipSuccess || splits == 1) return e;
   const bool r4 = (a.N & 3) == 0 && ((uintptr_t)a.ws & 15) == 0;
-  const unsigned rgrid4 = nblk((size_t)a.M * (a.N >> 2), kBlock);
-  switch (epi) {
-#define MYOS_GEMM_CASE(E)                                                          \
-  case E:                                                                         \
-    hipLaunchKernelGGL(gemm_mfma_kernel<E>, grid, dim3(kBlock), 0, s, a);         \
-    if (splits > 1 && r4)                                                         \
-      hipLaunchKernelGGL(gemm_reduce4_kernel<E>, dim3(rgrid4), dim3(kBlock), 0, s, a, splits); \
-    else if (splits > 1)                                                          \
-      hipLaunchKernelGGL(gemm_reduce_kernel<E>, dim3(rgrid), dim3(kBlock), 0, s, a, splits); \
-    break;
-    MYOS_GEMM_CASE(EPI_STORE)
-    MYOS_GEMM_CASE(EPI_RESID)
-    MYOS_GEMM_CASE(EPI_GU)
-    MYOS_GEMM_CASE(EPI_QKV)
-#undef MYOS_GEMM_CASE
-    default:
-      return hipErrorInvalidValue;
+  if (r4) {
+    const unsigned rgrid4 = nblk((size_t)a.M * (a.N >> 2), kBlock);
+    hipLaunchKernelGGL(gemm_reduce4_kernel<EPI>, dim3(rgrid4), dim3(kBlock), 0, s, a, splits);
+  } else {
+    const unsigned rgrid = nblk((size_t)a.M * ((a.N + 1) >> 1), kBlock);
+    hipLaunchKernelGGL(gemm_reduce_kernel<EPI>, dim3(rgrid), dim3(kBlock), 0, s, a, splits);
   }
   return hipGetLastError();
+}
+
+hipError_t launch_gemm(const GemmArgs &args, GemvEpi epi, hipStream_t s) {
+  if (args.M <= 0 || args.N <= 0) return hipSuccess;
+  switch (epi) {
+    case EPI_STORE: return launch_gemm_epi<EPI_STORE>(args, s);
+    case EPI_RESID: return launch_gemm_epi<EPI_RESID>(args, s);
+    case EPI_GU: return launch_gemm_epi<EPI_GU>(args, s);
+    case EPI_QKV: return launch_gemm_epi<EPI_QKV>(args, s);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 hipError_t launch_attn_prefill(const AttnPrefillArgs &a, hipStream_t s) {

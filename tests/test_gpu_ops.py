@@ -85,9 +85,13 @@ def test_gemv_order_cancellation():
     assert np.all(np.isin(got, [0.0, 1.0, 2.0, 3.0, 4.0]))
 
 
+# the planner's tile shapes: 128 x 32 split K (128, 1536, 1536), 128 x 64
+# split K (128, 1536, 8960), 128 x 128 split K with a row tail (37, 8960,
+# 1536), 128 x 64 and 128 x 256 over several row tiles with tails (1100,
+# 1536, 640), (1100, 4096, 256); K % 64 != 0 takes the fallback kernel
 @pytest.mark.parametrize("batch,m,k", [(128, 1536, 1536), (128, 256, 1536), (37, 8960, 1536),
-                                       (128, 1536, 8960), (5, 7, 3), (33, 70, 45),
-                                       (200, 130, 200)])
+                                       (128, 1536, 8960), (1100, 1536, 640), (1100, 4096, 256),
+                                       (5, 7, 3), (33, 70, 45), (200, 130, 200)])
 def test_gemm_vs_oracle(batch, m, k):
     rng = np.random.default_rng(batch + m + k)
     w = rand_w(rng, m, k)
