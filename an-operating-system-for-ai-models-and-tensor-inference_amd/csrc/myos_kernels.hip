@@ -365,6 +365,127 @@ __global__ void __launch_bounds__(kBlock) gemv_kernel(GemvArgs a) {
   }
 }
 
+// Streaming GEMV for large matrices: about two workgroups per CU, each
+// staging x once (with the fused RMSNorm for X_NORM) and then walking a
+// contiguous range of rows, RB rows per team at a time, while the team's
+// loads for its next RB rows are in flight. A one-shot launch (gemv_kernel)
+// stages x in every workgroup: with 16 or fewer rows per workgroup that
+// re-reads as many x bytes as weight bytes once k is large (a 3584 x 18944
+// down projection reads its 74 KB h vector 1792 times). The next batch is
+// always loaded (past the range: the range's first row again), so the
+// compiler's wait for the current batch leaves the next one in flight.
+template <int TEAM, int RB, int CPT, int XM, int EPI>
+__global__ void __launch_bounds__(kBlock) gemv_stream_kernel(GemvArgs a, int rows_per_wg) {
+  extern __shared__ float4 xs4[];
+  float *xs = (float *)xs4;
+  __shared__ float red4[4];
+  __shared__ float red[2][4][RB];
+  __shared__ float2 best[4];
+  constexpr int TEAMS = kBlock / TEAM;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int team = TEAMS == 1 ? 0 : wave;
+  const int tt = TEAMS == 1 ? tid : lane;
+  const int k = a.k, m = a.m, nch = k >> 3;
+  const int r0 = blockIdx.x * rows_per_wg, r1 = min(m, r0 + rows_per_wg);
+  const int nb = (r1 - r0 + RB - 1) / RB;  // batches of this workgroup
+  uint32_t pos = 0;
+  if (EPI == EPI_QKV) pos = *a.pos_ptr;
+
+  auto load = [&](u32x4 (&w)[RB][CPT], int b) {
+    const int rb = b < nb ? r0 + b * RB : r0;
+#pragma unroll
+    for (int r = 0; r < RB; r++) {
+      const u32x4 *rowp = (const u32x4 *)(a.w + (size_t)min(rb + r, m - 1) * k);
+#pragma unroll
+      for (int i = 0; i < CPT; i++) {
+        const int c = tt + i * TEAM;
+        const u32x4 zero = {0u, 0u, 0u, 0u};
+        w[r][i] = c < nch ? __builtin_nontemporal_load(rowp + c) : zero;
+      }
+    }
+  };
+  float bv = -INFINITY;
+  uint32_t bi = 0xffffffffu;
+  int parity = 0;
+  auto mult = [&](const u32x4 (&w)[RB][CPT], int b) {
+    float acc[RB];
+#pragma unroll
+    for (int r = 0; r < RB; r++) acc[r] = 0.f;
+#pragma unroll
+    for (int i = 0; i < CPT; i++) {
+      const int c = tt + i * TEAM;
+      if (c < nch) {
+        const float4 x0 = xs4[c * 2], x1 = xs4[c * 2 + 1];
+#pragma unroll
+        for (int r = 0; r < RB; r++) {
+          const u32x4 v = w[r][i];
+          float s = acc[r];
+          s = fmaf(bf_lo(v.x), x0.x, s);
+          s = fmaf(bf_hi(v.x), x0.y, s);
+          s = fmaf(bf_lo(v.y), x0.z, s);
+          s = fmaf(bf_hi(v.y), x0.w, s);
+          s = fmaf(bf_lo(v.z), x1.x, s);
+          s = fmaf(bf_hi(v.z), x1.y, s);
+          s = fmaf(bf_lo(v.w), x1.z, s);
+          s = fmaf(bf_hi(v.w), x1.w, s);
+          acc[r] = s;
+        }
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < RB; r++) acc[r] = group_sum<kWave>(acc[r]);
+    if (TEAMS == 1) {
+      // the four waves' sums through LDS; two buffers, so one barrier per batch
+      if (lane == 0) {
+#pragma unroll
+        for (int r = 0; r < RB; r++) red[parity][wave][r] = acc[r];
+      }
+      __syncthreads();
+#pragma unroll
+      for (int r = 0; r < RB; r++)
+        acc[r] = ((red[parity][0][r] + red[parity][1][r]) + red[parity][2][r]) + red[parity][3][r];
+      parity ^= 1;
+    }
+    if (tt == 0 && b < nb) {
+      const int row0 = r0 + b * RB;
+      float2 tb;
+      gemv_epilogue<EPI, RB>(a, row0, acc, pos, &tb);
+      if (EPI == EPI_HEAD && beats(tb.x, __float_as_uint(tb.y), bv, bi)) {
+        bv = tb.x;
+        bi = __float_as_uint(tb.y);
+      }
+    }
+  };
+
+  // weight loads first: they do not depend on x, so they overlap the staging
+  u32x4 wa[RB][CPT], wb[RB][CPT];
+  load(wa, team);
+  stage_x<XM>(a, xs, red4);
+  // every team runs the same number of batch pairs (the TEAM = 256 barrier)
+  const int steps = (nb + TEAMS - 1) / TEAMS;
+  for (int s = 0; s < steps; s += 2) {
+    const int b = team + s * TEAMS;
+    load(wb, b + TEAMS);
+    mult(wa, b);
+    if (s + 1 < steps) {
+      load(wa, b + 2 * TEAMS);
+      mult(wb, b + TEAMS);
+    }
+  }
+  if (EPI == EPI_HEAD) {
+    if (tt == 0) best[team] = make_float2(bv, __uint_as_float(bi));
+    __syncthreads();
+    if (tid == 0) {
+      float2 bb = best[0];
+#pragma unroll
+      for (int t = 1; t < TEAMS; t++)
+        if (beats(best[t].x, __float_as_uint(best[t].y), bb.x, __float_as_uint(bb.y))) bb = best[t];
+      a.part[blockIdx.x] = bb;
+      if (blockIdx.x == 0 && a.pos_inc) *a.pos_inc += 1u;
+    }
+  }
+}
+
 // Any k (including k % 8 != 0): one wavefront per row pair, element loads.
 template <int XM, int EPI>
 __global__ void __launch_bounds__(kBlock) gemv_generic_kernel(GemvArgs a) {
@@ -1424,6 +1545,7 @@ __global__ void __launch_bounds__(kTq * 8 * KG) attn_prefill_tiled_kernel(AttnPr
 }
 
 inline unsigned nblk(size_t n, unsigned b) { return (unsigned)((n + b - 1) / b); }
+constexpr long kCUsGemv = 256;
 
 }  // namespace
 
@@ -1459,6 +1581,72 @@ hipError_t go_gemv_generic(const GemvArgs &a, hipStream_t s, int *nparts) {
   return hipGetLastError();
 }
 
+// Streaming launch plan: a wavefront team (k <= 4096, chunks per lane
+// CPT <= 8, RB rows per batch) or a workgroup team (longer rows, RB = 2),
+// about two workgroups per CU, each taking a contiguous range of whole
+// batches. Taken for rows of >= 2048 columns in matrices of >= 32M weights
+// (measured on MI355X with the weights streamed from HBM: 3584 x 18944
+// 37.6 -> 31.5 us, 152064 x 3584 179 -> 169 us, 37888 x 3584 51.4 -> 50.5
+// us); smaller matrices and k = 1536 rows are faster one-shot (151936 x
+// 1536: 71.9 one-shot, 79.3 streaming).
+struct StreamPlan {
+  int team = 0, rb = 0, cpt = 0, grid = 0, rows_per_wg = 0;
+};
+int g_gemv_force = -1;  // -1 planner, 0 one-shot only, 1 streaming where it applies
+static StreamPlan stream_plan(int m, int k) {
+  StreamPlan p;
+  if (g_gemv_force == 0 || k % 8 != 0 || k < 8 || k > 24576 || m < 512) return p;
+  if (g_gemv_force < 0 && (k < 2048 || (size_t)m * k < (32u << 20))) return p;
+  const int nch = k / 8;
+  if (nch <= 64 * 8) {
+    p.team = 64;
+    p.cpt = (nch + 63) / 64;
+    if (p.cpt == 5) p.cpt = 6;
+    if (p.cpt == 7) p.cpt = 8;
+    p.rb = p.cpt <= 4 ? 4 : 2;
+  } else {
+    p.team = 256;
+    const int c = (nch + 255) / 256;
+    p.cpt = c <= 5 ? 5 : c <= 10 ? 10 : 12;
+    p.rb = 2;
+  }
+  const int teams = kBlock / p.team;
+  const long batches = (m + p.rb - 1) / p.rb;
+  const long wgs = std::min<long>(2 * kCUsGemv, (batches + teams - 1) / teams);
+  const long per = (batches + wgs - 1) / wgs;  // batches per workgroup
+  p.rows_per_wg = (int)(per * p.rb);
+  p.grid = (int)((m + p.rows_per_wg - 1) / p.rows_per_wg);
+  return p;
+}
+
+template <int TEAM, int RB, int CPT, int XM, int EPI>
+hipError_t go_stream(const GemvArgs &a, const StreamPlan &p, hipStream_t s, int *nparts) {
+  if (nparts) *nparts = p.grid;
+  if (EPI == EPI_HEAD && p.grid > a.part_cap) return hipErrorInvalidValue;
+  hipLaunchKernelGGL((gemv_stream_kernel<TEAM, RB, CPT, XM, EPI>), dim3(p.grid), dim3(kBlock),
+                     stage_bytes(a, XM), s, a, p.rows_per_wg);
+  return hipGetLastError();
+}
+
+template <int XM, int EPI>
+hipError_t pick_stream(const GemvArgs &a, const StreamPlan &p, hipStream_t s, int *nparts) {
+  if (p.team == 64) {
+    switch (p.cpt) {
+      case 1: return go_stream<64, 4, 1, XM, EPI>(a, p, s, nparts);
+      case 2: return go_stream<64, 4, 2, XM, EPI>(a, p, s, nparts);
+      case 3: return go_stream<64, 4, 3, XM, EPI>(a, p, s, nparts);
+      case 4: return go_stream<64, 4, 4, XM, EPI>(a, p, s, nparts);
+      case 6: return go_stream<64, 2, 6, XM, EPI>(a, p, s, nparts);
+      default: return go_stream<64, 2, 8, XM, EPI>(a, p, s, nparts);
+    }
+  }
+  switch (p.cpt) {
+    case 5: return go_stream<256, 2, 5, XM, EPI>(a, p, s, nparts);
+    case 10: return go_stream<256, 2, 10, XM, EPI>(a, p, s, nparts);
+    default: return go_stream<256, 2, 12, XM, EPI>(a, p, s, nparts);
+  }
+}
+
 // Variant choice: rows per team grow with m (more independent loads in flight
 // per lane); a wavefront team while one wave's chunks cover the row in <= 8
 // steps, else the whole workgroup splits the row (k up to 24576).
@@ -1468,6 +1656,10 @@ hipError_t pick_gemv(const GemvArgs &a, hipStream_t s, int *nparts) {
   const bool vec = (a.k % 8) == 0 && a.k >= 8 && ((uintptr_t)a.w % 16) == 0 &&
                    ((uintptr_t)a.x % 16) == 0 && (XM == X_PLAIN || ((uintptr_t)a.gamma % 8) == 0);
   if (!vec || a.k > 24576) return go_gemv_generic<XM, EPI>(a, s, nparts);
+  if (XM != X_ATTN) {
+    const StreamPlan p = stream_plan(a.m, a.k);
+    if (p.grid > 0) return pick_stream<XM, EPI>(a, p, s, nparts);
+  }
   const bool big = a.m >= 16384;
   if (nch <= 64 * 8) {
     const int cpt = (nch + 63) / 64;
@@ -1512,6 +1704,8 @@ hipError_t launch_gemv(const GemvArgs &a, GemvX xm, GemvEpi epi, hipStream_t s, 
 int gemv_head_parts(int m, int k) {
   const int nch = k / 8;
   if (k % 8 != 0 || k < 8 || k > 24576) return (int)nblk((size_t)m, 8);
+  const StreamPlan p = stream_plan(m, k);
+  if (p.grid > 0) return p.grid;
   const bool big = m >= 16384;
   if (nch <= 64 * 8) return (int)nblk((size_t)m, big ? 16 : 8);
   return (int)nblk((size_t)m, 2);
