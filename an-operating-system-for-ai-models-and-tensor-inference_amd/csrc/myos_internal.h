@@ -8,9 +8,8 @@
 namespace myos {
 
 // ---- GEMV family: one launch streams a row-major BF16 matrix once ----------
-// X_ATTN: x is the attention output, merged from the decode-attention
-// partials while it is staged (the o projection's prologue)
-enum GemvX { X_PLAIN = 0, X_NORM = 1, X_ATTN = 2 };
+// X_NORM: x goes through the RMSNorm with gains `gamma` as it is staged
+enum GemvX { X_PLAIN = 0, X_NORM = 1 };
 enum GemvEpi { EPI_STORE = 0, EPI_RESID = 1, EPI_QKV = 2, EPI_GU = 3, EPI_HEAD = 4 };
 
 struct GemvArgs {
@@ -34,9 +33,6 @@ struct GemvArgs {
   float2 *part = nullptr;       // x = value, y = index bits
   int part_cap = 0;             // entries `part` holds; a larger grid is refused
   uint32_t *pos_inc = nullptr;  // EPI_HEAD: block 0 increments *pos_inc when set
-  // X_ATTN: partials [nq][attn_nchunks][d + 2] = (o[d], m, l) per chunk
-  const float *attn_part = nullptr;
-  int attn_nchunks = 0, attn_nq = 0;
 };
 
 // Launch the best kernel variant for (m, k, x mode, epilogue); returns the
@@ -52,6 +48,8 @@ struct AttnDecodeArgs {
   int kv_bf16, max_seq, nq, nkv, head_dim;
   const uint32_t *pos_ptr; // attends positions 0..*pos_ptr
   float *part;             // out: [nq][nchunks][d + 2] per-chunk (o[d], m, l)
+  float *att;              // out: [nq * d] the merged attention output
+  int *cnt;                // [nkv] zero between launches: chunks finished per group
 };
 int attn_decode_chunks(int max_seq, int head_dim);
 size_t attn_decode_part_floats(int nq, int max_seq, int head_dim);

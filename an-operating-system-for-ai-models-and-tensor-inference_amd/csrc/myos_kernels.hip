@@ -117,85 +117,12 @@ __device__ float block_sum(float v, float *scratch4) {
 // applies the RMSNorm there (sum of squares over the whole vector, then
 // g * (x * inv_rms)), which fuses rmsnorm_bf16_weight into the projection.
 
-// the o-projection prologue merges at most this many attention outputs
-// (its LDS holds them)
-constexpr int kMaxAttnMergeK = 16 * kBlock;
-
 // decode attention splits positions into chunks of this many
 __host__ __device__ constexpr int attn_chunk(int d) { return d <= 128 ? 32 : 16; }
-
-// X_ATTN staging: the attention output of head h, lane j is
-//   sum_c w[h][c] o_c[h][j],  w[h][c] = e^(m_c - M_h) / sum_c' e^(m_c' - M_h) l_c'
-// over the chunks c that hold positions <= pos (the split-position softmax
-// recombined; gqa.rs:283-307 is the one-chunk case). All partial loads of a
-// step are independent, so they are issued together.
-__device__ void stage_attn(const GemvArgs &a, float *xs, float *ws) {
-  const int tid = threadIdx.x, d = a.head_dim, nq = a.attn_nq, nch = a.attn_nchunks;
-  const int ch = attn_chunk(d), nv = ((int)*a.pos_ptr + ch) / ch;
-  const size_t sp = (size_t)d + 2;
-  float *ms = ws, *ls = ws + nq * nv;
-  for (int i = tid; i < nq * nv; i += kBlock) {
-    const int h = i / nv, c = i - h * nv;
-    const float *src = a.attn_part + ((size_t)h * nch + c) * sp + d;
-    ms[i] = src[0];
-    ls[i] = src[1];
-  }
-  __syncthreads();
-  for (int h = tid; h < nq; h += kBlock) {
-    float mx = -INFINITY;
-    for (int c = 0; c < nv; c++) mx = fmaxf(mx, ms[h * nv + c]);
-    float l = 0.f;
-    for (int c = 0; c < nv; c++) {
-      const float w = expf(ms[h * nv + c] - mx);
-      ms[h * nv + c] = w;
-      l = fmaf(w, ls[h * nv + c], l);
-    }
-    const float inv = 1.0f / l;
-    for (int c = 0; c < nv; c++) ms[h * nv + c] *= inv;
-  }
-  __syncthreads();
-  // one wavefront per head; lane owns dims j and j + 64; chunk loads are
-  // unrolled by 8 so 16 independent loads are in flight per lane
-  const int lane = tid & 63, wave = tid >> 6;
-  for (int h = wave; h < nq; h += 4) {
-    const float *w = ms + h * nv;
-    const float *base = a.attn_part + (size_t)h * nch * sp;
-    for (int j0 = lane; j0 < d; j0 += 128) {
-      const int j1 = j0 + 64;
-      const bool two = j1 < d;
-      float acc0 = 0.f, acc1 = 0.f;
-      int c = 0;
-      for (; c + 8 <= nv; c += 8) {
-        float v0[8], v1[8];
-#pragma unroll
-        for (int u = 0; u < 8; u++) {
-          v0[u] = base[(size_t)(c + u) * sp + j0];
-          v1[u] = two ? base[(size_t)(c + u) * sp + j1] : 0.f;
-        }
-#pragma unroll
-        for (int u = 0; u < 8; u++) {
-          acc0 = fmaf(w[c + u], v0[u], acc0);
-          acc1 = fmaf(w[c + u], v1[u], acc1);
-        }
-      }
-      for (; c < nv; c++) {
-        acc0 = fmaf(w[c], base[(size_t)c * sp + j0], acc0);
-        if (two) acc1 = fmaf(w[c], base[(size_t)c * sp + j1], acc1);
-      }
-      xs[h * d + j0] = acc0;
-      if (two) xs[h * d + j1] = acc1;
-    }
-  }
-}
 
 template <int XM>
 __device__ void stage_x(const GemvArgs &a, float *xs, float *red4) {
   const int k = a.k, tid = threadIdx.x;
-  if (XM == X_ATTN) {
-    stage_attn(a, xs, xs + ((k + 3) & ~3));
-    __syncthreads();
-    return;
-  }
   float ss = 0.f;
   for (int j = tid * 4; j < k; j += kBlock * 4) {
     float4 v = *(const float4 *)(a.x + j);
@@ -501,14 +428,10 @@ __global__ void __launch_bounds__(kBlock) gemv_generic_kernel(GemvArgs a) {
   if (EPI == EPI_QKV) pos = *a.pos_ptr;
   // scalar staging (k may not be a multiple of 4)
   float ss = 0.f;
-  if (XM == X_ATTN) {
-    stage_attn(a, xs, xs + ((k + 3) & ~3));
-  } else {
-    for (int j = tid; j < k; j += kBlock) {
-      float v = a.x[j];
-      xs[j] = v;
-      ss += v * v;
-    }
+  for (int j = tid; j < k; j += kBlock) {
+    float v = a.x[j];
+    xs[j] = v;
+    ss += v * v;
   }
   if (XM == X_NORM) {
     float tot = block_sum(ss, red4);
@@ -568,7 +491,7 @@ __global__ void __launch_bounds__(kBlock) attn_decode_kernel(AttnDecodeArgs a) {
   const int seq = (int)*a.pos_ptr + 1;
   const int t0 = c * ch;
   const int n = min(ch, seq - t0);
-  if (n <= 0) return;  // past the cursor: the o-projection merges chunks < seq only
+  if (n <= 0) return;  // past the cursor: the merge takes chunks < seq only
   const float scale = 1.0f / sqrtf((float)d);
   for (int i = tid; i < gq * d; i += kBlock) q_s[i] = a.q[(size_t)g * gq * d + i];
   const size_t kv0 = ((size_t)g * a.max_seq + t0) * d;
@@ -627,13 +550,78 @@ __global__ void __launch_bounds__(kBlock) attn_decode_kernel(AttnDecodeArgs a) {
     const float *ph = p_s + h * ch;
     float o = 0.f;
     for (int t = 0; t < n; t++) o = fmaf(ph[t], v_s[t * d + j], o);
+    // device-coherent stores (they reach the coherence point, not this XCD's
+    // L2), so the merging workgroup on any XCD reads them with no cache flush
     float *dst = a.part + ((size_t)(g * gq + h) * nchunks + c) * stride_part;
-    dst[j] = o;
+    __hip_atomic_store(dst + j, o, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (j == 0) {
-      dst[d] = ml_s[2 * h];
-      dst[d + 1] = ml_s[2 * h + 1];
+      __hip_atomic_store(dst + d, ml_s[2 * h], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(dst + d + 1, ml_s[2 * h + 1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
+
+  // The last of the group's nv chunk workgroups to finish merges the group's
+  // heads: att[h] = sum_c w_c o_c with w_c = e^(m_c - M) / sum_c' e^(m_c' - M)
+  // l_c' (gqa.rs:283-307 is the one-chunk case), chunks added in order, so
+  // the result does not depend on which workgroup merges. The counter is
+  // reset by the merging workgroup for the next launch.
+  // Each thread waits until its partial stores have completed (vmcnt counts
+  // stores on gfx9; the asm is also a compiler barrier), then one thread
+  // counts the workgroup in. The merging workgroup reads the partials with
+  // device-coherent loads. No device-scope fence: on this part that writes
+  // back and invalidates the whole L2.
+  const int nv = (seq + ch - 1) / ch;
+  __shared__ int last_s;
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (tid == 0)
+    last_s = __hip_atomic_fetch_add(&a.cnt[g], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == nv - 1;
+  __syncthreads();
+  if (!last_s) return;
+  auto cload = [](const float *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  };
+  // each pass issues all of its loads before using them
+  float *wm = smem, *lm = smem + gq * nv;  // [gq][nv] (m, l) -> weights (the tiles are dead)
+  for (int i = tid; i < gq * nv; i += kBlock) {
+    const int h = i / nv, cc = i - h * nv;
+    const float *src = a.part + ((size_t)(g * gq + h) * nchunks + cc) * stride_part + d;
+    wm[i] = cload(src);
+    lm[i] = cload(src + 1);
+  }
+  __syncthreads();
+  for (int h = tid; h < gq; h += kBlock) {
+    float *w = wm + h * nv;
+    const float *lh = lm + h * nv;
+    float mx = -INFINITY;
+    for (int cc = 0; cc < nv; cc++) mx = fmaxf(mx, w[cc]);
+    float l = 0.f;
+    for (int cc = 0; cc < nv; cc++) {
+      const float e = expf(w[cc] - mx);
+      w[cc] = e;
+      l = fmaf(e, lh[cc], l);
+    }
+    const float inv = 1.0f / l;
+    for (int cc = 0; cc < nv; cc++) w[cc] *= inv;
+  }
+  __syncthreads();
+  for (int i = tid; i < gq * d; i += kBlock) {
+    const int h = i / d, j = i - h * d;
+    const float *w = wm + h * nv;
+    const float *base = a.part + (size_t)(g * gq + h) * nchunks * stride_part + j;
+    float acc = 0.f;
+    int cc = 0;
+    for (; cc + 8 <= nv; cc += 8) {
+      float v[8];
+#pragma unroll
+      for (int u = 0; u < 8; u++) v[u] = cload(base + (size_t)(cc + u) * stride_part);
+#pragma unroll
+      for (int u = 0; u < 8; u++) acc = fmaf(w[cc + u], v[u], acc);
+    }
+    for (; cc < nv; cc++) acc = fmaf(w[cc], cload(base + (size_t)cc * stride_part), acc);
+    a.att[(size_t)(g * gq + h) * d + j] = acc;
+  }
+  if (tid == 0) a.cnt[g] = 0;
 }
 
 // ----------------------------------------------------------- small ops ----
@@ -1552,13 +1540,8 @@ constexpr long kCUsGemv = 256;
 // ============================================================ launchers ====
 
 namespace {
-// dynamic LDS of a GEMV launch: x (k floats, rounded to 4) + the X_ATTN
-// merge weights (2 per head and chunk)
-size_t stage_bytes(const GemvArgs &a, int xm) {
-  size_t n = (size_t)((a.k + 3) & ~3);
-  if (xm == X_ATTN) n += 2 * (size_t)a.attn_nq * a.attn_nchunks;
-  return n * sizeof(float);
-}
+// dynamic LDS of a GEMV launch: x (k floats, rounded to 4)
+size_t stage_bytes(const GemvArgs &a, int) { return (size_t)((a.k + 3) & ~3) * sizeof(float); }
 
 template <int TEAM, int ROWS, int CPT, int XM, int EPI>
 hipError_t go_gemv(const GemvArgs &a, hipStream_t s, int *nparts) {
@@ -1581,9 +1564,7 @@ hipError_t go_gemv_generic(const GemvArgs &a, hipStream_t s, int *nparts) {
   return hipGetLastError();
 }
 
-// Streaming launch plan: a wavefront team (k <= 4096, chunks per lane
-// CPT <= 8, RB rows per batch) or a workgroup team (longer rows, RB = 2),
-// about two workgroups per CU, each taking a contiguous range of whole
+// Streaming launch plan: each workgroup takes a contiguous range of whole
 // batches. Taken for rows of >= 2048 columns in matrices of >= 32M weights
 // (measured on MI355X with the weights streamed from HBM: 3584 x 18944
 // 37.6 -> 31.5 us, 152064 x 3584 179 -> 169 us, 37888 x 3584 51.4 -> 50.5
@@ -1597,22 +1578,24 @@ static StreamPlan stream_plan(int m, int k) {
   StreamPlan p;
   if (g_gemv_force == 0 || k % 8 != 0 || k < 8 || k > 24576 || m < 512) return p;
   if (g_gemv_force < 0 && (k < 2048 || (size_t)m * k < (32u << 20))) return p;
+  // a workgroup team per row batch; measured best on MI355X: rows of <= 512
+  // chunks two at a time with ~4 workgroups per CU (37888 x 3584: 46.7 us),
+  // longer rows one at a time with 2 per CU (3584 x 18944: 29.9 us)
   const int nch = k / 8;
-  if (nch <= 64 * 8) {
-    p.team = 64;
-    p.cpt = (nch + 63) / 64;
-    if (p.cpt == 5) p.cpt = 6;
-    if (p.cpt == 7) p.cpt = 8;
-    p.rb = p.cpt <= 4 ? 4 : 2;
+  p.team = 256;
+  long cap;
+  if (nch <= 512) {
+    p.cpt = (nch + 255) / 256;
+    p.rb = 2;
+    cap = 4 * kCUsGemv;
   } else {
-    p.team = 256;
     const int c = (nch + 255) / 256;
     p.cpt = c <= 5 ? 5 : c <= 10 ? 10 : 12;
-    p.rb = 2;
+    p.rb = 1;
+    cap = 2 * kCUsGemv;
   }
-  const int teams = kBlock / p.team;
   const long batches = (m + p.rb - 1) / p.rb;
-  const long wgs = std::min<long>(2 * kCUsGemv, (batches + teams - 1) / teams);
+  const long wgs = std::min<long>(cap, batches);
   const long per = (batches + wgs - 1) / wgs;  // batches per workgroup
   p.rows_per_wg = (int)(per * p.rb);
   p.grid = (int)((m + p.rows_per_wg - 1) / p.rows_per_wg);
@@ -1630,20 +1613,12 @@ hipError_t go_stream(const GemvArgs &a, const StreamPlan &p, hipStream_t s, int 
 
 template <int XM, int EPI>
 hipError_t pick_stream(const GemvArgs &a, const StreamPlan &p, hipStream_t s, int *nparts) {
-  if (p.team == 64) {
-    switch (p.cpt) {
-      case 1: return go_stream<64, 4, 1, XM, EPI>(a, p, s, nparts);
-      case 2: return go_stream<64, 4, 2, XM, EPI>(a, p, s, nparts);
-      case 3: return go_stream<64, 4, 3, XM, EPI>(a, p, s, nparts);
-      case 4: return go_stream<64, 4, 4, XM, EPI>(a, p, s, nparts);
-      case 6: return go_stream<64, 2, 6, XM, EPI>(a, p, s, nparts);
-      default: return go_stream<64, 2, 8, XM, EPI>(a, p, s, nparts);
-    }
-  }
   switch (p.cpt) {
-    case 5: return go_stream<256, 2, 5, XM, EPI>(a, p, s, nparts);
-    case 10: return go_stream<256, 2, 10, XM, EPI>(a, p, s, nparts);
-    default: return go_stream<256, 2, 12, XM, EPI>(a, p, s, nparts);
+    case 1: return go_stream<256, 2, 1, XM, EPI>(a, p, s, nparts);
+    case 2: return go_stream<256, 2, 2, XM, EPI>(a, p, s, nparts);
+    case 5: return go_stream<256, 1, 5, XM, EPI>(a, p, s, nparts);
+    case 10: return go_stream<256, 1, 10, XM, EPI>(a, p, s, nparts);
+    default: return go_stream<256, 1, 12, XM, EPI>(a, p, s, nparts);
   }
 }
 
@@ -1656,10 +1631,8 @@ hipError_t pick_gemv(const GemvArgs &a, hipStream_t s, int *nparts) {
   const bool vec = (a.k % 8) == 0 && a.k >= 8 && ((uintptr_t)a.w % 16) == 0 &&
                    ((uintptr_t)a.x % 16) == 0 && (XM == X_PLAIN || ((uintptr_t)a.gamma % 8) == 0);
   if (!vec || a.k > 24576) return go_gemv_generic<XM, EPI>(a, s, nparts);
-  if (XM != X_ATTN) {
-    const StreamPlan p = stream_plan(a.m, a.k);
-    if (p.grid > 0) return pick_stream<XM, EPI>(a, p, s, nparts);
-  }
+  const StreamPlan p = stream_plan(a.m, a.k);
+  if (p.grid > 0) return pick_stream<XM, EPI>(a, p, s, nparts);
   const bool big = a.m >= 16384;
   if (nch <= 64 * 8) {
     const int cpt = (nch + 63) / 64;
@@ -1691,10 +1664,8 @@ hipError_t pick_gemv(const GemvArgs &a, hipStream_t s, int *nparts) {
 
 hipError_t launch_gemv(const GemvArgs &a, GemvX xm, GemvEpi epi, hipStream_t s, int *nparts) {
   if (a.m <= 0) return hipSuccess;
-  if (xm == X_ATTN && a.k > kMaxAttnMergeK) return hipErrorInvalidValue;
   if (xm == X_PLAIN && epi == EPI_STORE) return pick_gemv<X_PLAIN, EPI_STORE>(a, s, nparts);
   if (xm == X_PLAIN && epi == EPI_RESID) return pick_gemv<X_PLAIN, EPI_RESID>(a, s, nparts);
-  if (xm == X_ATTN && epi == EPI_RESID) return pick_gemv<X_ATTN, EPI_RESID>(a, s, nparts);
   if (xm == X_NORM && epi == EPI_QKV) return pick_gemv<X_NORM, EPI_QKV>(a, s, nparts);
   if (xm == X_NORM && epi == EPI_GU) return pick_gemv<X_NORM, EPI_GU>(a, s, nparts);
   if (xm == X_NORM && epi == EPI_HEAD) return pick_gemv<X_NORM, EPI_HEAD>(a, s, nparts);
@@ -2063,7 +2034,8 @@ hipError_t launch_transpose_u32(uint32_t *dst, const uint32_t *src, int rows, in
 const char *kernel_build_info() {
   return "gfx950; gemv: wave/workgroup teams, 16B nontemporal bf16 loads, fused "
          "rmsnorm/bias+rope+kv/swiglu/residual/argmax epilogues; attention: split-position "
-         "decode partials merged in the o-projection prologue; prefill: v_mfma_f32_32x32x16_bf16 hi/lo GEMM";
+         "decode partials merged by the last chunk workgroup of each kv group; streaming GEMV for "
+         "large projections; prefill: v_mfma_f32_32x32x16_bf16 hi/lo GEMM, LDS-pipelined, planned tiles";
 }
 
 }  // namespace myos

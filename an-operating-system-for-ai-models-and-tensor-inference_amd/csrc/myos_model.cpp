@@ -71,6 +71,7 @@ struct myos_model {
   size_t ws_bytes = 0;
   float *x = nullptr, *q = nullptr, *att = nullptr, *h = nullptr, *logits = nullptr,
         *normed = nullptr, *attn_part = nullptr;
+  int *attn_cnt = nullptr;  // per kv group: chunk workgroups finished (decode attention merge)
   float2 *part = nullptr;
   int nparts = 0;
   uint32_t *state = nullptr, *out_ids = nullptr;
@@ -224,19 +225,17 @@ int enq_kernel(myos_model *m, int which, size_t l, bool advance_pos) {
       ad.head_dim = (int)s.head_dim;
       ad.pos_ptr = m->state;
       ad.part = m->attn_part;
+      ad.att = m->att;
+      ad.cnt = m->attn_cnt;
       return hs(launch_attn_decode(ad, st));
     }
-    case MYOS_K_O:
+    case MYOS_K_O:  // the attention kernel left the merged heads in att
       g.w = L.wo;
-      g.attn_part = m->attn_part;
-      g.attn_nchunks = attn_decode_chunks((int)m->max_seq, (int)s.head_dim);
-      g.attn_nq = (int)s.num_q_heads;
-      g.head_dim = (int)s.head_dim;
-      g.pos_ptr = m->state;
+      g.x = m->att;
       g.m = (int)s.hidden;
       g.k = (int)m->q_dim;
       g.y = m->x;
-      return hs(launch_gemv(g, X_ATTN, EPI_RESID, st));
+      return hs(launch_gemv(g, X_PLAIN, EPI_RESID, st));
     case MYOS_K_GATE_UP:
       g.w = L.wgu;
       g.x = m->x;
@@ -799,7 +798,8 @@ static int open_impl(myos_model *m, const char *path, const myos_block_shape *sh
       align256(attn_decode_part_floats((int)s.num_q_heads, (int)max_seq, (int)s.head_dim) * 4);
   const size_t b_st = align256(16);
   const size_t b_ids = align256(max_seq * 4);
-  m->ws_bytes = 2 * b_x + 2 * b_q + b_h + b_lg + b_part + b_ap + b_st + 2 * b_ids;
+  const size_t b_cnt = align256(s.num_kv_heads * 4);
+  m->ws_bytes = 2 * b_x + 2 * b_q + b_h + b_lg + b_part + b_ap + b_st + 2 * b_ids + b_cnt;
   HIP_TRY(hipMalloc((void **)&m->ws, m->ws_bytes));
   HIP_TRY(hipMemsetAsync(m->ws, 0, m->ws_bytes, m->stream));
   p = m->ws;
@@ -824,6 +824,8 @@ static int open_impl(myos_model *m, const char *path, const myos_block_shape *sh
   m->out_ids = (uint32_t *)p;
   p += b_ids;
   m->force_ids = (uint32_t *)p;
+  p += b_ids;
+  m->attn_cnt = (int *)p;  // zero (the memset above); each attention launch leaves it zero
   // argmax of the all-zero logits BlockWorkspace starts with is id 0
   std::vector<float2> part0(m->nparts);
   uint32_t none = 0xffffffffu, zero = 0;
