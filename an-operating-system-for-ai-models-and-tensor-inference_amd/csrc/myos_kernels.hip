@@ -1532,6 +1532,285 @@ __global__ void __launch_bounds__(kTq * 8 * KG) attn_prefill_tiled_kernel(AttnPr
   }
 }
 
+// Causal prefill attention on MFMA, head_dim 128 (v_mfma_f32_32x32x16_bf16).
+// Workgroup = (query head h, 128 queries): four waves of 32 queries; the
+// head's key/value rows stream through LDS in blocks of 32 keys (two stages,
+// the next block loaded into registers while the current one is multiplied).
+// Per block and wave:
+//   S^T = K Q^T (32 keys x 32 queries, 8 steps over the head dims): lane l
+//     then holds 16 scores of query l % 32 (keys 8 (i / 4) + 4 (l / 32) +
+//     i % 4), so a query's max and sum over the block are its lane's 16
+//     values and one exchange with lane l ^ 32;
+//   O^T += V^T P^T (4 tiles of 32 dims, 2 steps over the keys): the B
+//     operand is the lane's own probabilities, because V^T sits in LDS with
+//     each 16-key step's keys in the order the S^T layout hands them out
+//     (position 8 half + 4 (j / 4) + j % 4 holds key 8 (j / 4) + 4 half +
+//     j % 4), and the lane's O^T column is its own query, so the online
+//     softmax rescale is lane-local.
+// f32 operands enter as bf16 hi + lo pairs, three products each (hi hi,
+// lo hi, hi lo), about 16 significant bits, accumulated in f32. Query i sits
+// at position start + i and sees keys <= it (GqaMask::Causal, gqa.rs:80-86).
+constexpr int kFaQ = 128, kFaK = 32, kFaD = 128;
+constexpr int kFaStage = 4 * kFaK * kFaD * 2;  // K hi, K lo, V^T hi, V^T lo (bf16)
+constexpr int kFaLds = 2 * kFaStage + kFaK * kFaD * 4;  // + the f32 V staging tile
+
+// V^T position of key kk (0..31) of a block
+__device__ __forceinline__ int fa_vpos(int kk) {
+  return (kk & 16) + (((kk >> 2) & 1) << 3) + (((kk >> 3) & 1) << 2) + (kk & 3);
+}
+
+__global__ void __launch_bounds__(256) attn_prefill_mfma_kernel(AttnPrefillArgs a) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t fa_sm[];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int h = blockIdx.x, g = h / (a.nq / a.nkv);
+  const int q0 = blockIdx.y * kFaQ;
+  const int qi = q0 + wave * 32 + (lane & 31);  // this lane's query
+  const bool active = qi < a.M;
+  const int qpos = a.start_pos + (active ? qi : a.M - 1);
+  const int last_pos = a.start_pos + min(a.M - 1, q0 + kFaQ - 1);  // the workgroup's last query
+  const int wave_last = a.start_pos + min(a.M - 1, q0 + wave * 32 + 31);
+  const int nblk = last_pos / kFaK + 1;
+  // scores scaled by log2(e) / sqrt(d): the softmax runs on exp2
+  const float scale2 = 1.4426950408889634f / sqrtf((float)kFaD);
+  const int qd = a.nq * kFaD;
+
+  // Q^T operand of the score MFMA: lane l, step ks -> query l % 32, dims
+  // 16 ks + 8 (l / 32) .. + 7
+  bf16x8 qh[8], ql[8];
+  {
+    const float *qrow = a.q + (size_t)(active ? qi : a.M - 1) * qd + h * kFaD + 8 * (lane >> 5);
+#pragma unroll
+    for (int ks = 0; ks < 8; ks++) {
+      const float4 x0 = *(const float4 *)(qrow + 16 * ks), x1 = *(const float4 *)(qrow + 16 * ks + 4);
+      const float v[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        const __bf16 hb = (__bf16)v[e];
+        qh[ks][e] = hb;
+        ql[ks][e] = (__bf16)(v[e] - (float)hb);
+      }
+    }
+  }
+
+  // block loader: thread t takes key t / 8 of the block, dims (t % 8) 16 .. + 15
+  const int lkey = tid >> 3, ldim = (tid & 7) * 16;
+  float kr[16], vr[16];
+  auto gload = [&](int b) {
+    const int kpos = min(b * kFaK + lkey, last_pos);
+    const size_t base = ((size_t)g * a.max_seq + kpos) * kFaD + ldim;
+    if (a.kv_bf16) {
+#pragma unroll
+      for (int u = 0; u < 2; u++) {
+        const u32x4 kb = *(const u32x4 *)((const uint16_t *)a.kc + base + 8 * u);
+        const u32x4 vb = *(const u32x4 *)((const uint16_t *)a.vc + base + 8 * u);
+        const uint32_t kw[4] = {kb.x, kb.y, kb.z, kb.w}, vw[4] = {vb.x, vb.y, vb.z, vb.w};
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          kr[8 * u + 2 * e] = bf_lo(kw[e]);
+          kr[8 * u + 2 * e + 1] = bf_hi(kw[e]);
+          vr[8 * u + 2 * e] = bf_lo(vw[e]);
+          vr[8 * u + 2 * e + 1] = bf_hi(vw[e]);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int u = 0; u < 4; u++) {
+        const float4 k4 = *(const float4 *)((const float *)a.kc + base + 4 * u);
+        const float4 v4 = *(const float4 *)((const float *)a.vc + base + 4 * u);
+        kr[4 * u] = k4.x; kr[4 * u + 1] = k4.y; kr[4 * u + 2] = k4.z; kr[4 * u + 3] = k4.w;
+        vr[4 * u] = v4.x; vr[4 * u + 1] = v4.y; vr[4 * u + 2] = v4.z; vr[4 * u + 3] = v4.w;
+      }
+    }
+  };
+  // K rows: 256 B (16 chunks of 8 dims), chunk c at slot c ^ (key & 15).
+  // V goes through an f32 row-major staging tile (float4 stores), then each
+  // thread gathers 16 keys of one dim from it (lanes on consecutive dims, no
+  // bank conflicts) into two 8-key octets of the V^T row.
+  // V^T rows: 64 B (4 octets of keys), octet o at slot o ^ ((dim >> 2) & 3).
+  float *vstage = (float *)(fa_sm + 2 * kFaStage);  // [kFaK][kFaD] f32
+  auto sstore_k = [&](int st) {
+    uint8_t *kh = fa_sm + st * kFaStage, *kl = kh + kFaK * kFaD * 2;
+#pragma unroll
+    for (int u = 0; u < 2; u++) {
+      bf16x8 hi, lo;
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        const float v = kr[8 * u + e];
+        const __bf16 hb = (__bf16)v;
+        hi[e] = hb;
+        lo[e] = (__bf16)(v - (float)hb);
+      }
+      const int c = (ldim >> 3) + u, off = lkey * 256 + ((c ^ (lkey & 15)) << 4);
+      *(bf16x8 *)(kh + off) = hi;
+      *(bf16x8 *)(kl + off) = lo;
+    }
+#pragma unroll
+    for (int u = 0; u < 4; u++)
+      *(float4 *)(vstage + lkey * kFaD + ldim + 4 * u) =
+          make_float4(vr[4 * u], vr[4 * u + 1], vr[4 * u + 2], vr[4 * u + 3]);
+  };
+  // thread t: dim t / 2, key step t & 1 (keys 16 s .. 16 s + 15); octet 0 of
+  // the step holds keys {0..3, 8..11}, octet 1 keys {4..7, 12..15}
+  auto sstore_vt = [&](int st) {
+    uint8_t *vh = fa_sm + st * kFaStage + 2 * kFaK * kFaD * 2, *vl = vh + kFaK * kFaD * 2;
+    const int dim = tid >> 1, s2 = tid & 1;
+#pragma unroll
+    for (int oc = 0; oc < 2; oc++) {
+      bf16x8 hi, lo;
+#pragma unroll
+      for (int j = 0; j < 8; j++) {
+        const int key = 16 * s2 + 8 * (j >> 2) + 4 * oc + (j & 3);
+        const float v = vstage[key * kFaD + dim];
+        const __bf16 hb = (__bf16)v;
+        hi[j] = hb;
+        lo[j] = (__bf16)(v - (float)hb);
+      }
+      const int off = dim * 64 + (((2 * s2 + oc) ^ ((dim >> 2) & 3)) << 4);
+      *(bf16x8 *)(vh + off) = hi;
+      *(bf16x8 *)(vl + off) = lo;
+    }
+  };
+
+  f32x16 o[4];
+#pragma unroll
+  for (int n = 0; n < 4; n++)
+#pragma unroll
+    for (int e = 0; e < 16; e++) o[n][e] = 0.f;
+  float mx = -INFINITY, l = 0.f;
+
+  gload(0);
+  sstore_k(0);
+  gload(1);
+  __syncthreads();
+  sstore_vt(0);
+  __syncthreads();
+  for (int b = 0; b < nblk; b++) {
+    const int st = b & 1;
+    const int kb = b * kFaK;
+    if (kb <= wave_last) {  // some query of the wave sees a key of the block
+      const uint8_t *kh = fa_sm + st * kFaStage, *kl = kh + kFaK * kFaD * 2;
+      const uint8_t *vh = kl + kFaK * kFaD * 2, *vl = vh + kFaK * kFaD * 2;
+      // three independent chains (hi hi, lo hi, hi lo) keep the MFMA pipe busy
+      f32x16 s0, s1, s2;
+#pragma unroll
+      for (int e = 0; e < 16; e++) {
+        s0[e] = 0.f;
+        s1[e] = 0.f;
+        s2[e] = 0.f;
+      }
+      const int krow = (lane & 31) * 256;
+#pragma unroll
+      for (int ks = 0; ks < 8; ks++) {
+        const int c = 2 * ks + (lane >> 5), off = krow + ((c ^ (lane & 15)) << 4);
+        const bf16x8 ah = *(const bf16x8 *)(kh + off), al = *(const bf16x8 *)(kl + off);
+        s0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, qh[ks], s0, 0, 0, 0);
+        s1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, qh[ks], s1, 0, 0, 0);
+        s2 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, ql[ks], s2, 0, 0, 0);
+      }
+      // scores in the base-2 domain: s log2(e) / sqrt(d), masked; block max
+      float sc[16];
+      float bm = -INFINITY;
+#pragma unroll
+      for (int i = 0; i < 16; i++) {
+        const int key = kb + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
+        sc[i] = key <= qpos ? ((s0[i] + s1[i]) + s2[i]) * scale2 : -INFINITY;
+        bm = fmaxf(bm, sc[i]);
+      }
+      bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
+      const float mnew = fmaxf(mx, bm);
+      float p[16];
+      float ps = 0.f;
+      if (mnew != -INFINITY) {
+        const float corr = __builtin_amdgcn_exp2f(mx - mnew);  // mx = -inf: 0
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+          p[i] = __builtin_amdgcn_exp2f(sc[i] - mnew);  // masked: 2^-inf = 0
+          ps += p[i];
+        }
+        ps += __shfl_xor(ps, 32, 64);
+        l = l * corr + ps;
+        mx = mnew;
+        // the accumulators leave the matrix registers only when some query of
+        // the wave raised its max
+        if (__builtin_amdgcn_ballot_w64(corr != 1.0f)) {
+#pragma unroll
+          for (int n = 0; n < 4; n++)
+#pragma unroll
+            for (int e = 0; e < 16; e++) o[n][e] *= corr;
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < 16; i++) p[i] = 0.f;
+      }
+      // P^T operand for key step s2: the lane's probabilities 8 s2 .. 8 s2 + 7
+#pragma unroll
+      for (int s2 = 0; s2 < 2; s2++) {
+        bf16x8 ph, pl;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+          const float v = p[8 * s2 + e];
+          const __bf16 hb = (__bf16)v;
+          ph[e] = hb;
+          pl[e] = (__bf16)(v - (float)hb);
+        }
+        const int oct = 2 * s2 + (lane >> 5);
+#pragma unroll
+        for (int n = 0; n < 4; n++) {
+          const int dim = 32 * n + (lane & 31);
+          const int off = dim * 64 + ((oct ^ ((dim >> 2) & 3)) << 4);
+          const bf16x8 vah = *(const bf16x8 *)(vh + off), val = *(const bf16x8 *)(vl + off);
+          o[n] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vah, ph, o[n], 0, 0, 0);
+          o[n] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(val, ph, o[n], 0, 0, 0);
+          o[n] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vah, pl, o[n], 0, 0, 0);
+        }
+      }
+    }
+    // block b + 1 into the other stage (its last readers passed the previous
+    // barrier); the V staging tile is free again after each transpose's barrier
+    if (b + 1 < nblk) sstore_k(st ^ 1);
+    gload(b + 2);  // always issued (clamped past the last block)
+    __syncthreads();
+    if (b + 1 < nblk) {
+      sstore_vt(st ^ 1);
+      __syncthreads();
+    }
+  }
+  // O^T tile n: lane l holds dims 32 n + 8 (i / 4) + 4 (l / 32) + i % 4 of
+  // its query. The normalised rows go to LDS (the stages are free after the
+  // last barrier), then each lane writes 8 consecutive dims of one query as
+  // 16-byte hi / lo stores.
+  float *orow = (float *)fa_sm + wave * 32 * (kFaD + 4);  // [32][d + 4] f32 per wave
+  const float inv = 1.0f / l;
+#pragma unroll
+  for (int n = 0; n < 4; n++)
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+      const int dim = 32 * n + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
+      orow[(lane & 31) * (kFaD + 4) + dim] = o[n][i] * inv;
+    }
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < 8; r++) {
+    const int qq = r * 4 + (lane >> 4), c8 = (lane & 15) * 8;  // query of the wave, dims c8 .. + 7
+    const int qrow = q0 + wave * 32 + qq;
+    if (qrow < a.M) {
+      const float *src = orow + qq * (kFaD + 4) + c8;
+      const float4 x0 = *(const float4 *)src, x1 = *(const float4 *)(src + 4);
+      const float v[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+      bf16x8 hi, lo;
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        const __bf16 hb = (__bf16)v[e];
+        hi[e] = hb;
+        lo[e] = (__bf16)(v[e] - (float)hb);
+      }
+      const size_t idx = (size_t)qrow * qd + h * kFaD + c8;
+      *(bf16x8 *)(a.out_hi + idx) = hi;
+      *(bf16x8 *)(a.out_lo + idx) = lo;
+    }
+  }
+}
+
 inline unsigned nblk(size_t n, unsigned b) { return (unsigned)((n + b - 1) / b); }
 constexpr long kCUsGemv = 256;
 
@@ -1976,6 +2255,18 @@ hipError_t launch_gemm(const GemmArgs &args, GemvEpi epi, hipStream_t s) {
 
 hipError_t launch_attn_prefill(const AttnPrefillArgs &a, hipStream_t s) {
   if (a.head_dim > kMaxHeadDim) return hipErrorInvalidValue;
+  if (a.head_dim == kFaD && a.nq % a.nkv == 0) {
+    static bool attr_done = false;
+    const void *fn = (const void *)attn_prefill_mfma_kernel;
+    if (!attr_done) {
+      hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, kFaLds);
+      if (e != hipSuccess) return e;
+      attr_done = true;
+    }
+    AttnPrefillArgs args = a;
+    void *params[] = {&args};
+    return hipLaunchKernel(fn, dim3(a.nq, nblk((size_t)a.M, kFaQ)), dim3(256), params, kFaLds, s);
+  }
   // 16-byte tile loads: the cache rows and q must be aligned to 4 elements
   if (a.head_dim == 128 || a.head_dim == 64 || a.head_dim == 32) {
     dim3 tg(a.nq, nblk((size_t)a.M, kTq));
