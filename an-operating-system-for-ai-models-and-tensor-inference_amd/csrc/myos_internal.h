@@ -118,7 +118,8 @@ struct GemmArgs {
   int kps;                     // set by the launcher: K steps per split
 };
 // Launch plan of the pipelined MFMA GEMM: tile shape (cfg 0..3 = 128 x 32,
-// 64, 128, 256; -1 = the shape needs the fallback kernel) and K splits
+// 64, 128, 256) and K splits; cfg -1 takes the single-stage 128 x 64 kernel
+// (shapes the pipelined one does not take, and wide short-K projections)
 struct GemmPlan {
   int cfg = -1;
   int splits = 1;
