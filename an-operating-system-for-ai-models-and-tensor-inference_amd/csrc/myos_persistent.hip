@@ -731,7 +731,10 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
           // Later steps read the cache rows without tags, so they must be
           // complete before anything this wave publishes later. Every later
           // publish follows one of the wave's gathers, and the wait for a
-          // gather's loads (vmcnt 0) also waits for these stores.
+          // gather's loads (vmcnt 0) also waits for these stores (gfx9 counts
+          // stores in vmcnt). The empty asm with a memory clobber keeps the
+          // compiler from sinking the stores past that wait.
+          asm volatile("" ::: "memory");
         }
       }
 

@@ -86,12 +86,13 @@ def test_gemv_order_cancellation():
 
 
 # the planner's tile shapes: 128 x 32 split K (128, 1536, 1536), 128 x 64
-# split K (128, 1536, 8960), 128 x 128 split K with a row tail (37, 8960,
-# 1536), 128 x 64 and 128 x 256 over several row tiles with tails (1100,
-# 1536, 640), (1100, 4096, 256); K % 64 != 0 takes the fallback kernel
+# split K (128, 1536, 8960), 128 x 64 over several row tiles with tails
+# (1100, 1536, 640), 128 x 128 (600, 4096, 512), 128 x 256 (1100, 4096, 256);
+# the single-stage kernel for a wide short-K shape with a row tail (37, 8960,
+# 1536) and for K % 64 != 0
 @pytest.mark.parametrize("batch,m,k", [(128, 1536, 1536), (128, 256, 1536), (37, 8960, 1536),
                                        (128, 1536, 8960), (1100, 1536, 640), (1100, 4096, 256),
-                                       (5, 7, 3), (33, 70, 45), (200, 130, 200)])
+                                       (600, 4096, 512), (5, 7, 3), (33, 70, 45), (200, 130, 200)])
 def test_gemm_vs_oracle(batch, m, k):
     rng = np.random.default_rng(batch + m + k)
     w = rand_w(rng, m, k)
