@@ -478,6 +478,240 @@ __global__ void __launch_bounds__(kBlock) gemv_generic_kernel(GemvArgs a) {
 constexpr int kMaxQPerKv = 8;
 constexpr int kMaxHeadDim = 256;
 
+// The last of a group's nv chunk workgroups to finish merges the group's
+// heads. Each thread first waits until its partial stores have completed
+// (vmcnt counts stores on gfx9; the asm is also a compiler barrier), then one
+// thread counts the workgroup in with a relaxed device-scope add. The merging
+// workgroup reads the partials with device-coherent loads. No device-scope
+// fence: on this part that writes back and invalidates the whole L2.
+__device__ bool attn_last_in_group(const AttnDecodeArgs &a, int g, int nv) {
+  __shared__ int last_s;
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (threadIdx.x == 0)
+    last_s = __hip_atomic_fetch_add(&a.cnt[g], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == nv - 1;
+  __syncthreads();
+  return last_s != 0;
+}
+
+// Device-coherent (sc1, the cache policy of a relaxed agent-scope atomic
+// load) 32-bit load of element i through a buffer descriptor. To the
+// compiler it is an ordinary load, so a run of them goes out back to back:
+// every atomic load orders the memory operations around it, which put a full
+// wait after each one (a merge of 30 partials took 30 round trips).
+__device__ __forceinline__ float attn_cload(__amdgpu_buffer_rsrc_t rs, size_t i) {
+  return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, (int)(i * 4), 0, 16));
+}
+
+// Merge of group g's nv chunk partials ([nq][nchunks][d + 2]: o, m, l):
+// att[h] = sum_c w_c o_c with w_c = e^(m_c - M) / sum_c' e^(m_c' - M) l_c'
+// (gqa.rs:283-307 is the one-chunk case), chunks added in order, so the
+// result does not depend on which workgroup merges. The counter is reset for
+// the next launch. With at most kFastMerge chunks every load is issued in one
+// round trip (this thread's o values into registers, every (m, l) into LDS);
+// longer runs load the weights first and the o values in batches of 8.
+constexpr int kFastMerge = 16;
+__device__ void attn_merge(const AttnDecodeArgs &a, int g, int gq, int d, int nv, int nchunks,
+                           float *smem) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const size_t stride = (size_t)d + 2;
+  const float *part = a.part + (size_t)g * gq * nchunks * stride;
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+      (void *)part, (short)0, (int)((size_t)gq * nchunks * stride * 4), 0x00020000);
+  const int nout = gq * d;
+  float *wm = smem, *lm = smem + gq * nv;  // [gq][nv] (m, l) -> weights
+  auto load_ml = [&]() {
+    for (int i = tid; i < gq * nv; i += kBlock) {
+      const int h = i / nv, cc = i - h * nv;
+      const size_t src = ((size_t)h * nchunks + cc) * stride + d;
+      wm[i] = attn_cload(rs, src);
+      lm[i] = attn_cload(rs, src + 1);
+    }
+  };
+  if (nv <= kFastMerge && nout <= 4 * kBlock) {
+    float ov[4][kFastMerge];
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const int i = tid + r * kBlock, h = i / d, j = i - h * d;
+#pragma unroll
+      for (int cc = 0; cc < kFastMerge; cc++)
+        ov[r][cc] = i < nout && cc < nv ? attn_cload(rs, ((size_t)h * nchunks + cc) * stride + j) : 0.f;
+    }
+    load_ml();
+    __syncthreads();
+    // one wave per head: lane cc holds chunk cc
+    for (int h = wave; h < gq; h += kBlock / kWave) {
+      const float m = lane < nv ? wm[h * nv + lane] : -INFINITY;
+      const float mx = group_max<kWave>(m);
+      const float e = lane < nv ? expf(m - mx) : 0.f;
+      const float l = group_sum<kWave>(lane < nv ? e * lm[h * nv + lane] : 0.f);
+      if (lane < nv) wm[h * nv + lane] = e * (1.0f / l);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const int i = tid + r * kBlock, h = i / d, j = i - h * d;
+      if (i < nout) {
+        float acc = 0.f;
+#pragma unroll
+        for (int cc = 0; cc < kFastMerge; cc++)
+          if (cc < nv) acc = fmaf(wm[h * nv + cc], ov[r][cc], acc);
+        a.att[(size_t)(g * gq + h) * d + j] = acc;
+      }
+    }
+  } else {
+    load_ml();
+    __syncthreads();
+    for (int h = tid; h < gq; h += kBlock) {
+      float *w = wm + h * nv;
+      const float *lh = lm + h * nv;
+      float mx = -INFINITY;
+      for (int cc = 0; cc < nv; cc++) mx = fmaxf(mx, w[cc]);
+      float l = 0.f;
+      for (int cc = 0; cc < nv; cc++) {
+        const float e = expf(w[cc] - mx);
+        w[cc] = e;
+        l = fmaf(e, lh[cc], l);
+      }
+      const float inv = 1.0f / l;
+      for (int cc = 0; cc < nv; cc++) w[cc] *= inv;
+    }
+    __syncthreads();
+    for (int i = tid; i < nout; i += kBlock) {
+      const int h = i / d, j = i - h * d;
+      const float *w = wm + h * nv;
+      const size_t base = (size_t)h * nchunks * stride + j;
+      float acc = 0.f;
+      int cc = 0;
+      for (; cc + 8 <= nv; cc += 8) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) v[u] = attn_cload(rs, base + (size_t)(cc + u) * stride);
+#pragma unroll
+        for (int u = 0; u < 8; u++) acc = fmaf(w[cc + u], v[u], acc);
+      }
+      for (; cc < nv; cc++) acc = fmaf(w[cc], attn_cload(rs, base + (size_t)cc * stride), acc);
+      a.att[(size_t)(g * gq + h) * d + j] = acc;
+    }
+  }
+  if (tid == 0) a.cnt[g] = 0;
+}
+
+// Decode attention at head_dim 128 with the chunk in registers: workgroup
+// (kv head g, chunk c of 32 positions); thread (wave w, lane l) holds
+// positions t = 8 w + 4 (l >> 5) + u, u < 4, columns [4 (l & 31), +4) of K
+// and V, and the same columns of the group's gq query heads. A score is a
+// 32-lane sum (DPP); wave w then takes the softmax of heads w, w + 4; the V
+// sum runs on the same registers, its 8 partial sums per column (two lane
+// halves x four waves) added through LDS in a fixed order. Same partial
+// layout and merge as attn_decode_kernel.
+template <bool KB>
+__global__ void __launch_bounds__(kBlock) attn_decode_d128_kernel(AttnDecodeArgs a) {
+  constexpr int D = 128, CH = 32;
+  extern __shared__ float smem[];
+  float4 *o_s = (float4 *)smem;                // [4 waves][2 halves][gq][32]: V-sum partials
+  float *p_s = smem + 4 * 2 * kMaxQPerKv * D;  // [gq][CH] scores -> weights
+  float *ml_s = p_s + kMaxQPerKv * CH;         // [gq][2]
+  const int gq = a.nq / a.nkv, g = blockIdx.x, c = blockIdx.y, nchunks = gridDim.y;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, half = lane >> 5, j4 = lane & 31;
+  const int seq = (int)*a.pos_ptr + 1, t0 = c * CH, n = min(CH, seq - t0);
+  if (n <= 0) return;  // past the cursor: the merge takes chunks < seq only
+  const size_t row0 = (size_t)g * a.max_seq + t0;
+  float4 kr[4], vr[4];
+#pragma unroll
+  for (int u = 0; u < 4; u++) {
+    const int t = 8 * wave + 4 * half + u;
+    kr[u] = vr[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (t < n) {
+      const size_t e = (row0 + t) * D + 4 * j4;
+      if (KB) {
+        const uint2 k2 = *(const uint2 *)((const uint16_t *)a.kc + e);
+        const uint2 v2 = *(const uint2 *)((const uint16_t *)a.vc + e);
+        kr[u] = make_float4(bf_lo(k2.x), bf_hi(k2.x), bf_lo(k2.y), bf_hi(k2.y));
+        vr[u] = make_float4(bf_lo(v2.x), bf_hi(v2.x), bf_lo(v2.y), bf_hi(v2.y));
+      } else {
+        kr[u] = *(const float4 *)((const float *)a.kc + e);
+        vr[u] = *(const float4 *)((const float *)a.vc + e);
+      }
+    }
+  }
+  float4 q4[kMaxQPerKv];
+#pragma unroll
+  for (int h = 0; h < kMaxQPerKv; h++)
+    if (h < gq) q4[h] = *(const float4 *)(a.q + (size_t)(g * gq + h) * D + 4 * j4);
+  const float scale = 1.0f / sqrtf((float)D);
+#pragma unroll
+  for (int h = 0; h < kMaxQPerKv; h++) {
+    if (h >= gq) break;
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+      float s = q4[h].x * kr[u].x;
+      s = fmaf(q4[h].y, kr[u].y, s);
+      s = fmaf(q4[h].z, kr[u].z, s);
+      s = fmaf(q4[h].w, kr[u].w, s);
+      s = group_sum<16>(s);
+      s += dpp<0x142, 0xA>(s, 0.f);  // rows 1, 3 add rows 0, 2: lanes 16-31, 48-63 hold the 32-lane sums
+      const int t = 8 * wave + 4 * half + u;
+      if ((lane & 31) == 16 && t < n) p_s[h * CH + t] = s * scale;
+    }
+  }
+  __syncthreads();
+  for (int h = wave; h < gq; h += kBlock / kWave) {
+    const float s = lane < n ? p_s[h * CH + lane] : -INFINITY;
+    const float mx = group_max<kWave>(s);
+    const float e = lane < n ? expf(s - mx) : 0.f;
+    const float l = group_sum<kWave>(e);
+    if (lane < CH) p_s[h * CH + lane] = e;
+    if (lane == 0) {
+      ml_s[2 * h] = mx;
+      ml_s[2 * h + 1] = l;
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int h = 0; h < kMaxQPerKv; h++) {
+    if (h >= gq) break;
+    const float4 e4 = *(const float4 *)(p_s + h * CH + 8 * wave + 4 * half);
+    const float ev[4] = {e4.x, e4.y, e4.z, e4.w};
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+      acc.x = fmaf(ev[u], vr[u].x, acc.x);
+      acc.y = fmaf(ev[u], vr[u].y, acc.y);
+      acc.z = fmaf(ev[u], vr[u].z, acc.z);
+      acc.w = fmaf(ev[u], vr[u].w, acc.w);
+    }
+    o_s[((wave * 2 + half) * kMaxQPerKv + h) * 32 + j4] = acc;
+  }
+  __syncthreads();
+  const size_t stride = (size_t)D + 2;
+  for (int i = tid; i < gq * 32; i += kBlock) {
+    const int h = i >> 5, jj = i & 31;
+    float4 o = o_s[h * 32 + jj];
+#pragma unroll
+    for (int p = 1; p < 8; p++) {
+      const float4 v = o_s[(p * kMaxQPerKv + h) * 32 + jj];
+      o.x += v.x;
+      o.y += v.y;
+      o.z += v.z;
+      o.w += v.w;
+    }
+    // device-coherent stores (they reach the coherence point, not this XCD's
+    // L2), so the merging workgroup on any XCD reads them with no cache flush
+    float *dst = a.part + ((size_t)(g * gq + h) * nchunks + c) * stride;
+    __hip_atomic_store(dst + 4 * jj, o.x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(dst + 4 * jj + 1, o.y, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(dst + 4 * jj + 2, o.z, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(dst + 4 * jj + 3, o.w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (jj == 0) {
+      __hip_atomic_store(dst + D, ml_s[2 * h], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(dst + D + 1, ml_s[2 * h + 1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+  const int nv = (seq + CH - 1) / CH;
+  if (attn_last_in_group(a, g, nv)) attn_merge(a, g, gq, D, nv, nchunks, smem);
+}
+
 __global__ void __launch_bounds__(kBlock) attn_decode_kernel(AttnDecodeArgs a) {
   extern __shared__ float smem[];
   const int d = a.head_dim, gq = a.nq / a.nkv, dp = d + 1, ch = attn_chunk(d);
@@ -560,68 +794,7 @@ __global__ void __launch_bounds__(kBlock) attn_decode_kernel(AttnDecodeArgs a) {
     }
   }
 
-  // The last of the group's nv chunk workgroups to finish merges the group's
-  // heads: att[h] = sum_c w_c o_c with w_c = e^(m_c - M) / sum_c' e^(m_c' - M)
-  // l_c' (gqa.rs:283-307 is the one-chunk case), chunks added in order, so
-  // the result does not depend on which workgroup merges. The counter is
-  // reset by the merging workgroup for the next launch.
-  // Each thread waits until its partial stores have completed (vmcnt counts
-  // stores on gfx9; the asm is also a compiler barrier), then one thread
-  // counts the workgroup in. The merging workgroup reads the partials with
-  // device-coherent loads. No device-scope fence: on this part that writes
-  // back and invalidates the whole L2.
-  const int nv = (seq + ch - 1) / ch;
-  __shared__ int last_s;
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
-  if (tid == 0)
-    last_s = __hip_atomic_fetch_add(&a.cnt[g], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == nv - 1;
-  __syncthreads();
-  if (!last_s) return;
-  auto cload = [](const float *p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  };
-  // each pass issues all of its loads before using them
-  float *wm = smem, *lm = smem + gq * nv;  // [gq][nv] (m, l) -> weights (the tiles are dead)
-  for (int i = tid; i < gq * nv; i += kBlock) {
-    const int h = i / nv, cc = i - h * nv;
-    const float *src = a.part + ((size_t)(g * gq + h) * nchunks + cc) * stride_part + d;
-    wm[i] = cload(src);
-    lm[i] = cload(src + 1);
-  }
-  __syncthreads();
-  for (int h = tid; h < gq; h += kBlock) {
-    float *w = wm + h * nv;
-    const float *lh = lm + h * nv;
-    float mx = -INFINITY;
-    for (int cc = 0; cc < nv; cc++) mx = fmaxf(mx, w[cc]);
-    float l = 0.f;
-    for (int cc = 0; cc < nv; cc++) {
-      const float e = expf(w[cc] - mx);
-      w[cc] = e;
-      l = fmaf(e, lh[cc], l);
-    }
-    const float inv = 1.0f / l;
-    for (int cc = 0; cc < nv; cc++) w[cc] *= inv;
-  }
-  __syncthreads();
-  for (int i = tid; i < gq * d; i += kBlock) {
-    const int h = i / d, j = i - h * d;
-    const float *w = wm + h * nv;
-    const float *base = a.part + (size_t)(g * gq + h) * nchunks * stride_part + j;
-    float acc = 0.f;
-    int cc = 0;
-    for (; cc + 8 <= nv; cc += 8) {
-      float v[8];
-#pragma unroll
-      for (int u = 0; u < 8; u++) v[u] = cload(base + (size_t)(cc + u) * stride_part);
-#pragma unroll
-      for (int u = 0; u < 8; u++) acc = fmaf(w[cc + u], v[u], acc);
-    }
-    for (; cc < nv; cc++) acc = fmaf(w[cc], cload(base + (size_t)cc * stride_part), acc);
-    a.att[(size_t)(g * gq + h) * d + j] = acc;
-  }
-  if (tid == 0) a.cnt[g] = 0;
+  if (attn_last_in_group(a, g, (seq + ch - 1) / ch)) attn_merge(a, g, gq, d, (seq + ch - 1) / ch, nchunks, smem);
 }
 
 // ----------------------------------------------------------- small ops ----
@@ -1972,11 +2145,21 @@ size_t attn_decode_part_floats(int nq, int max_seq, int head_dim) {
 hipError_t launch_attn_decode(const AttnDecodeArgs &a, hipStream_t s) {
   const int gq = a.nq / a.nkv, d = a.head_dim;
   if (gq > kMaxQPerKv || d > kMaxHeadDim) return hipErrorInvalidValue;
-  const int ch = attn_chunk(d);
-  const size_t smem = sizeof(float) * ((size_t)gq * d + (size_t)ch * (d + 1) + (size_t)ch * d +
-                                       (size_t)gq * ch + 2 * gq);
+  const int ch = attn_chunk(d), nchunks = attn_decode_chunks(a.max_seq, d);
+  const size_t merge = sizeof(float) * 2 * (size_t)gq * nchunks;  // the merge's (m, l) table
+  dim3 grid(a.nkv, nchunks);
+  if (d == 128) {
+    const size_t smem = std::max(merge, sizeof(float) * (4 * 2 * kMaxQPerKv * 128 + kMaxQPerKv * 34));
+    if (smem > 65536) return hipErrorInvalidValue;
+    if (a.kv_bf16)
+      hipLaunchKernelGGL(attn_decode_d128_kernel<true>, grid, dim3(kBlock), smem, s, a);
+    else
+      hipLaunchKernelGGL(attn_decode_d128_kernel<false>, grid, dim3(kBlock), smem, s, a);
+    return hipGetLastError();
+  }
+  const size_t smem = std::max(merge, sizeof(float) * ((size_t)gq * d + (size_t)ch * (d + 1) +
+                                                       (size_t)ch * d + (size_t)gq * ch + 2 * gq));
   if (smem > 65536) return hipErrorInvalidValue;
-  dim3 grid(a.nkv, attn_decode_chunks(a.max_seq, d));
   hipLaunchKernelGGL(attn_decode_kernel, grid, dim3(kBlock), smem, s, a);
   return hipGetLastError();
 }
