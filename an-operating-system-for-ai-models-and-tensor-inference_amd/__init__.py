@@ -36,7 +36,7 @@ KIND = {
 }
 
 KV_F32, KV_BF16 = 0, 1
-DECODE_AUTO, DECODE_KERNELS, DECODE_PERSISTENT = 0, 1, 2
+DECODE_AUTO, DECODE_KERNELS, DECODE_PERSISTENT, DECODE_STREAMED = 0, 1, 2, 3
 SHAPE_QWEN25_1_5B, SHAPE_QWEN25_7B = 0, 1
 
 
@@ -400,7 +400,8 @@ class Model:
         _check(lib().myos_set_graph(self._h, 1 if on else 0), "set_graph")
 
     def set_decode_mode(self, mode: int):
-        """DECODE_AUTO / DECODE_KERNELS / DECODE_PERSISTENT for greedy_decode."""
+        """DECODE_AUTO / DECODE_KERNELS / DECODE_PERSISTENT / DECODE_STREAMED for
+        greedy_decode."""
         _check(lib().myos_set_decode_mode(self._h, int(mode)), "set_decode_mode")
 
     def set_decode_trace(self, step: int):
@@ -417,7 +418,8 @@ class Model:
         return out
 
     def decode_path(self) -> int:
-        """DECODE_KERNELS or DECODE_PERSISTENT: the path greedy_decode takes."""
+        """DECODE_KERNELS, DECODE_PERSISTENT or DECODE_STREAMED: the path
+        greedy_decode takes."""
         return int(lib().myos_decode_path(self._h))
 
     def last_prefill_ms(self) -> float:

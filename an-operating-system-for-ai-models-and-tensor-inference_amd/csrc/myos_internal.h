@@ -183,6 +183,10 @@ struct PersistArgs {
   int kv_bf16;                 // the cache at kc / vc holds bf16
   uint64_t *trace;             // optional [grid][5 L + 3] phase timestamps of one step
   uint32_t trace_step;
+  // streamed kernel: f32 activation buffers (wide_buffer_floats) and one
+  // barrier flag word per workgroup (zeroed once; tags only grow)
+  float *wide;
+  uint64_t *wflags;
 };
 int persist_grid();                       // workgroups per launch
 int persist_tags_per_step(int layers);
@@ -190,6 +194,11 @@ size_t persist_part_words(int nq, int max_seq, int d);
 bool persist_supported(int H, int I, int qdim, int d, int gq);
 bool persist_device_ok(const PersistArgs &a);  // shape, LDS and the current device fit
 hipError_t launch_decode_persistent(const PersistArgs &a, hipStream_t s);
+// the streamed cooperative kernel, for layers larger than the chip holds
+bool wide_supported(int H, int I, int qdim, int d, int gq, int max_seq);
+size_t wide_buffer_floats(int H, int I, int nq, int d, int max_seq);
+bool wide_device_ok(const PersistArgs &a);
+hipError_t launch_decode_wide(const PersistArgs &a, hipStream_t s);
 
 // dst[c][r] = src[r][c] for a [rows, cols] matrix of 32-bit words
 hipError_t launch_transpose_u32(uint32_t *dst, const uint32_t *src, int rows, int cols,

@@ -93,7 +93,8 @@ struct myos_model {
   double prefill_ms = 0, decode_ms = 0;
   // persistent decode: one cooperative launch per greedy_decode call
   int decode_mode = MYOS_DECODE_AUTO;
-  bool persist_ok = false;        // shape, KV dtype and device allow it
+  bool persist_ok = false;        // the register-resident cooperative kernel fits
+  bool wide_ok = false;           // the streamed cooperative kernel fits
   uint8_t *pbuf = nullptr;        // tagged exchange words + error word, zeroed
   size_t pbuf_bytes = 0;
   PersistLayer *dlayers = nullptr;
@@ -429,36 +430,51 @@ int setup_persistent(myos_model *m) {
   a.eps = s.rms_eps;
   a.kv_bf16 = m->kv_bf16;
   a.tpr = nullptr;
-  if (!persist_device_ok(a)) return MYOS_OK;
-  const size_t words[8] = {m->q_dim, 2 * m->kv_dim, persist_part_words(a.nq, a.max_seq, a.d),
-                           m->q_dim, s.hidden, s.hidden, 2 * (size_t)persist_grid(),
-                           (size_t)persist_grid() * persist_grid() *
-                               ((s.hidden + persist_grid() - 1) / persist_grid())};
+  const bool reg = persist_device_ok(a);
+  const bool wide = wide_device_ok(a);
+  if (!reg && !wide) return MYOS_OK;
+  // the register kernel's tagged words (none without it), the streamed
+  // kernel's f32 buffers and barrier flags (none without it), the error word
+  size_t words[8] = {m->q_dim, 2 * m->kv_dim, persist_part_words(a.nq, a.max_seq, a.d),
+                     m->q_dim, s.hidden, s.hidden, 2 * (size_t)persist_grid(),
+                     (size_t)persist_grid() * persist_grid() *
+                         ((s.hidden + persist_grid() - 1) / persist_grid())};
+  if (!reg)
+    for (size_t &w : words) w = 0;
+  const size_t wide_f = wide ? wide_buffer_floats(a.H, a.I, a.nq, a.d, a.max_seq) : 0;
+  const size_t flags = wide ? (size_t)persist_grid() : 0;
   size_t total = 0;
   for (size_t w : words) total += align256(w * 8);
-  total += 256;  // error word
+  total += align256(wide_f * 4) + align256(flags * 8) + 256;
   HIP_TRY(hipMalloc((void **)&m->pbuf, total));
   HIP_TRY(hipMemsetAsync(m->pbuf, 0, total, m->stream));
   m->pbuf_bytes = total;
   uint64_t **dst[8] = {&a.tq, &a.tkv, &a.tpart, &a.tatt, &a.txo, &a.txd, &a.targ, &a.tpr};
   uint8_t *p = m->pbuf;
   for (int i = 0; i < 8; i++) {
-    *dst[i] = (uint64_t *)p;
+    *dst[i] = words[i] ? (uint64_t *)p : nullptr;
     p += align256(words[i] * 8);
   }
+  a.wide = wide ? (float *)p : nullptr;
+  p += align256(wide_f * 4);
+  a.wflags = wide ? (uint64_t *)p : nullptr;
+  p += align256(flags * 8);
   m->err = (uint32_t *)p;
   a.err = m->err;
   std::vector<PersistLayer> hl(s.num_layers);
   const size_t dsz = s.intermediate * s.hidden;  // elements of one down matrix
-  // the cooperative kernel reads down by columns: a copy of it as column
-  // pairs (one 32-bit word per row of a pair)
-  HIP_TRY(hipMalloc((void **)&m->wdp, s.num_layers * dsz * 2));
-  for (size_t l = 0; l < s.num_layers; l++)
-    HIP_TRY(launch_transpose_u32(m->wdp + l * dsz / 2, (const uint32_t *)m->layers[l].wd,
-                                 (int)s.hidden, (int)s.intermediate / 2, m->stream));
+  // the register kernel reads down by columns: a copy of it as column pairs
+  // (one 32-bit word per row of a pair); the streamed kernel reads rows
+  if (reg) {
+    HIP_TRY(hipMalloc((void **)&m->wdp, s.num_layers * dsz * 2));
+    for (size_t l = 0; l < s.num_layers; l++)
+      HIP_TRY(launch_transpose_u32(m->wdp + l * dsz / 2, (const uint32_t *)m->layers[l].wd,
+                                   (int)s.hidden, (int)s.intermediate / 2, m->stream));
+  }
   for (size_t l = 0; l < s.num_layers; l++) {
     const DevLayer &L = m->layers[l];
-    hl[l] = PersistLayer{L.ln1, L.wqkv, L.wo, L.ln2, L.wgu, L.wd, L.bqkv, m->wdp + l * dsz / 2};
+    hl[l] = PersistLayer{L.ln1, L.wqkv, L.wo, L.ln2, L.wgu, L.wd, L.bqkv,
+                         reg ? m->wdp + l * dsz / 2 : nullptr};
   }
   HIP_TRY(hipMalloc((void **)&m->dlayers, hl.size() * sizeof(PersistLayer)));
   HIP_TRY(hipMemcpy(m->dlayers, hl.data(), hl.size() * sizeof(PersistLayer),
@@ -481,14 +497,24 @@ int setup_persistent(myos_model *m) {
   a.state = m->state;
   a.out_ids = m->out_ids;
   a.force = nullptr;
-  m->persist_ok = true;
+  m->persist_ok = reg;
+  m->wide_ok = wide;
   return MYOS_OK;
 }
 
 constexpr int kLaunchRefused = -1;
 
+// the streamed kernel runs when asked for, or when the register kernel does
+// not fit the model
+bool use_wide(const myos_model *m) {
+  if (m->decode_mode == MYOS_DECODE_KERNELS) return false;
+  if (m->decode_mode == MYOS_DECODE_STREAMED) return m->wide_ok;
+  return !m->persist_ok && m->wide_ok;
+}
+
 bool use_persistent(const myos_model *m) {
-  return m->persist_ok && m->decode_mode != MYOS_DECODE_KERNELS;
+  if (m->decode_mode == MYOS_DECODE_KERNELS) return false;
+  return use_wide(m) || m->persist_ok;
 }
 
 // n greedy steps from the cursor in one cooperative launch; the error word
@@ -505,11 +531,12 @@ int persist_decode(myos_model *m, size_t n, bool forced = false) {
   a.steps = (uint32_t)n;
   a.pos0 = (uint32_t)m->len;
   a.force = forced ? m->force_ids : nullptr;
-  if (m->trace_step >= 0 && (size_t)m->trace_step < n) {
+  if (m->trace_step >= 0 && (size_t)m->trace_step < n && !use_wide(m)) {
     a.trace = m->trace;
     a.trace_step = (uint32_t)m->trace_step;
   }
-  const hipError_t e = launch_decode_persistent(a, m->stream);
+  const hipError_t e = use_wide(m) ? launch_decode_wide(a, m->stream)
+                                    : launch_decode_persistent(a, m->stream);
   if (e == hipErrorCooperativeLaunchTooLarge || e == hipErrorInvalidConfiguration) {
     (void)hipGetLastError();
     return kLaunchRefused;  // nothing ran: the caller takes the per-kernel path
@@ -545,6 +572,7 @@ int decode_run(myos_model *m, size_t n, uint32_t mode, uint32_t *out) {
   if (rc == kLaunchRefused) {
     // the device cannot hold the cooperative grid: per-kernel path from now on
     m->persist_ok = false;
+    m->wide_ok = false;
     persist = false;
     prepare_graph(m);
     HIP_TRY(hipEventRecord(m->ev0, m->stream));
@@ -1137,8 +1165,9 @@ int myos_kv_read(const myos_model *m, size_t layer, size_t head, size_t pos, flo
 }
 
 int myos_set_decode_mode(myos_model *m, int mode) {
-  if (!m || mode < MYOS_DECODE_AUTO || mode > MYOS_DECODE_PERSISTENT) return MYOS_E_ARG;
-  if (mode == MYOS_DECODE_PERSISTENT && !m->persist_ok) return MYOS_E_SHAPE;
+  if (!m || mode < MYOS_DECODE_AUTO || mode > MYOS_DECODE_STREAMED) return MYOS_E_ARG;
+  if (mode == MYOS_DECODE_PERSISTENT && !m->persist_ok && !m->wide_ok) return MYOS_E_SHAPE;
+  if (mode == MYOS_DECODE_STREAMED && !m->wide_ok) return MYOS_E_SHAPE;
   m->decode_mode = mode;
   return MYOS_OK;
 }
@@ -1161,7 +1190,7 @@ int myos_set_decode_trace(myos_model *m, int64_t step) {
 
 int myos_debug_raise_wait_error(myos_model *m) {
   if (!m) return MYOS_E_ARG;
-  if (!m->persist_ok) return MYOS_E_SHAPE;
+  if (!m->persist_ok && !m->wide_ok) return MYOS_E_SHAPE;
   const uint32_t one = 1;
   HIP_TRY(hipMemcpyAsync(m->err, &one, 4, hipMemcpyHostToDevice, m->stream));
   HIP_TRY(hipStreamSynchronize(m->stream));
@@ -1179,7 +1208,8 @@ int myos_copy_decode_trace(const myos_model *m, uint64_t *out, size_t n) {
 
 int myos_decode_path(const myos_model *m) {
   if (!m) return MYOS_E_ARG;
-  return use_persistent(m) ? MYOS_DECODE_PERSISTENT : MYOS_DECODE_KERNELS;
+  if (!use_persistent(m)) return MYOS_DECODE_KERNELS;
+  return use_wide(m) ? MYOS_DECODE_STREAMED : MYOS_DECODE_PERSISTENT;
 }
 
 int myos_set_graph(myos_model *m, int enabled) {

@@ -19,6 +19,8 @@
 // always drains. The reference's numerics are the same as the per-kernel path
 // (crates/model_core/src/qwen25_block.rs:220-304 per step).
 #include <hip/hip_runtime.h>
+
+#include <algorithm>
 #include <math.h>
 #include <stdint.h>
 
@@ -1167,6 +1169,894 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
   }
 }
 
+// ============================================================================
+// Streamed cooperative decode, for shapes whose layer the chip cannot hold
+// (the 7B shape: 466 MB of weights per layer, 1.8 MB per CU).
+//
+// One cooperative launch of 256 workgroups (512 threads) runs a greedy_decode
+// call like decode_persistent_kernel, but every phase streams its weight rows
+// from HBM with the next row batch in flight, and phases meet at device-wide
+// barriers: a workgroup waits until its own stores have completed, publishes
+// a tagged flag word, and waits until all 256 flags carry the tag (or a later
+// one). Before each barrier every wave issues the loads of its first row
+// batch of the next phase (weights do not depend on the data), so the weight
+// stream keeps running across the wait. Activations cross workgroups through
+// f32 buffers with device-coherent (sc1) stores and loads. A layer is six
+// phases:
+//   QKV rows (+ bias, RoPE, KV-cache store) | attention items (kv head,
+//   32-position chunk) | merge per q head | o rows (+ residual) | RMSNorm +
+//   gate/up rows (+ SwiGLU) | down rows (+ residual)
+// then per step the final norm, the head rows with per-workgroup argmax
+// partials and the argmax, which every workgroup takes from the partials.
+// Numerics follow the per-kernel path: f32 FMAs over the bf16 weights in the
+// same row orders (qwen25_block.rs:220-304 per step).
+constexpr int WDC = 5;    // 8-column chunks per thread of a down row: I <= 20480
+constexpr int WMR = 16;   // residual rows per workgroup: H <= 4096
+constexpr int WRB = 2;    // rows per wave batch
+constexpr int WXMAX = 4096;  // LDS floats of the phase input vector
+constexpr int WMAXQ = 8;     // q heads per kv head
+constexpr int WQP = 64;      // QKV rows per workgroup
+constexpr int WMCH = 64;     // attention chunks per head (one lane each in the merge)
+constexpr int WOR = 32;      // o rows per workgroup
+constexpr int WLMAX = 128;   // layers (the layer table sits in LDS)
+// barrier tags of a layer, in the order the phases run (a flag is compared
+// with >=, so they must grow)
+constexpr uint32_t W_QKV = 0, W_PART = 1, W_ATT = 2, W_XO = 3, W_H = 4, W_X = 5;
+static_assert(W_X < kTPL, "six barriers per layer");
+
+__host__ __device__ inline size_t wide_al(size_t n) { return (n + 63) & ~(size_t)63; }
+
+// LDS floats of the attention staging (q, V, scores)
+__host__ __device__ inline int wide_big_floats(int d, int max_seq) {
+  (void)d;
+  (void)max_seq;
+  return WMAXQ * MAXD + AC * MAXD + WMAXQ * AC;
+}
+
+// workgroups [0, n) run the attention items and hold no o rows, when every
+// step's items fit in a quarter of the grid (else 0: o rows everywhere)
+__host__ __device__ inline int wide_item_wgs(int nkv, int nchmax) {
+  return nkv * nchmax <= NB / 4 ? nkv * nchmax : 0;
+}
+
+// f32 activation buffers of the streamed kernel, carved from one allocation
+struct WideBufs {
+  float *q, *att, *x, *xo, *h, *part, *arg;
+  int *cnt;        // per kv group: attention items done this layer (the last one merges)
+  uint32_t *tick;  // gate/up tile tickets handed out this launch
+};
+__host__ __device__ inline size_t wide_part_floats(int nq, int max_seq, int d) {
+  return (size_t)nq * ((max_seq + AC - 1) / AC) * (size_t)(d + 2);
+}
+__host__ __device__ inline WideBufs wide_bufs(float *base, int H, int I, int nq, int d, int max_seq,
+                                             size_t *total) {
+  WideBufs b;
+  const size_t qd = (size_t)nq * d;
+  size_t o = 0;
+  b.q = base + o;    o += wide_al(qd);
+  b.att = base + o;  o += wide_al(qd);
+  b.x = base + o;    o += wide_al(H);
+  b.xo = base + o;   o += wide_al(H);
+  b.h = base + o;    o += wide_al(I);
+  b.part = base + o; o += wide_al(wide_part_floats(nq, max_seq, d));
+  b.arg = base + o;  o += wide_al(2 * NB);
+  b.cnt = (int *)(base + o); o += wide_al(WMAXQ * 64);
+  b.tick = (uint32_t *)(base + o); o += wide_al(1);
+  if (total) *total = o;
+  return b;
+}
+
+// device-coherent (sc1) 32-bit load of float i of the buffer at p: an
+// ordinary load to the compiler, so a run of them goes out back to back (a
+// relaxed atomic load would take a full wait after each one)
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t crsrc(const void *p) {
+  return __builtin_amdgcn_make_buffer_rsrc((void *)p, (short)0, 0x7fffffff, 0x00020000);
+}
+// a plain buffer descriptor over p (loads through it are scalar-addressed)
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t gsrc(const void *p) {
+  return __builtin_amdgcn_make_buffer_rsrc((void *)p, (short)0, 0x7fffffff, 0x00020000);
+}
+__device__ __forceinline__ float cldb(__amdgpu_buffer_rsrc_t rs, int byte_off) {
+  return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, byte_off, 0, 16));
+}
+__device__ __forceinline__ float cld(__amdgpu_buffer_rsrc_t rs, int i) {
+  return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, i * 4, 0, 16));
+}
+
+// Device-wide barrier `tag`: this workgroup's stores are complete (vmcnt
+// counts stores on gfx9) before thread 0 publishes the flag; `pf` then issues
+// the next phase's weight loads (after the flag, so the wait for the stores
+// does not also wait for them), and thread t < NB waits until flag t carries
+// the tag or a later one (a workgroup can be one barrier ahead, never two).
+// Returns false when a wait gave up.
+template <class Pf>
+__device__ __forceinline__ bool wide_barrier(const PersistArgs &a, uint32_t tag, int *fail, Pf pf) {
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (threadIdx.x == 0) tput(a.wflags + blockIdx.x, 0.f, tag);
+  pf();
+  bool ok = *fail == 0;
+  if (threadIdx.x < NB && ok) {
+    for (unsigned spins = 0;; spins++) {
+      const uint64_t w = tload(a.wflags + threadIdx.x);
+      if ((uint32_t)(w >> 32) >= tag) break;
+      if (spin_fail(a, spins)) {
+        ok = false;
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+    }
+  }
+  if (!ok) *fail = 1;
+  __syncthreads();
+  return *fail == 0;
+}
+
+// n floats of a device-coherent buffer into LDS, every load issued first
+// (n <= 8 NT)
+__device__ __forceinline__ void cload_vec(float *dst, const float *src, int n, int tid) {
+  const __amdgpu_buffer_rsrc_t rs = crsrc(src);
+  float v[8];
+#pragma unroll
+  for (int u = 0; u < 8; u++) {
+    const int i = tid + u * NT;
+    v[u] = cld(rs, i < n ? i : 0);
+  }
+#pragma unroll
+  for (int u = 0; u < 8; u++) {
+    const int i = tid + u * NT;
+    if (i < n) dst[i] = v[u];
+  }
+}
+
+// a batch of WRB consecutive rows from `row` (clamped to `last`), 8 columns
+// per chunk per lane; every load is issued on every path
+template <int C>
+__device__ __forceinline__ void wld(u32x4 (&t)[WRB][C], const uint16_t *W, int k, int row, int last,
+                                    int lane) {
+#pragma unroll
+  for (int rb = 0; rb < WRB; rb++) ldrow_all<C>(t[rb], W, k, row + rb, last, lane);
+}
+
+// RMSNorm of x (LDS, k floats) into this lane's chunks (lane + 64 i), f32;
+// the bf16 gains g in global memory or LDS
+template <int C>
+__device__ __forceinline__ void wnorm(float4 (&xr)[C][2], const float *x, const uint16_t *g, int k,
+                                      float eps, int lane) {
+  load_x<C>(xr, x, k, lane);
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < C; i++) {
+    const float4 p = xr[i][0], q = xr[i][1];
+    ss += p.x * p.x + p.y * p.y + p.z * p.z + p.w * p.w + q.x * q.x + q.y * q.y + q.z * q.z + q.w * q.w;
+  }
+  const float inv = 1.0f / sqrtf(wave_sum(ss) / (float)k + eps);
+  const int nch = k >> 3;
+#pragma unroll
+  for (int i = 0; i < C; i++) {
+    const int c = lane + i * 64;
+    if (c < nch) {
+      const u32x4 gw = *(const u32x4 *)(g + c * 8);
+      xr[i][0] = make_float4(bf_lo(gw.x) * (xr[i][0].x * inv), bf_hi(gw.x) * (xr[i][0].y * inv),
+                             bf_lo(gw.y) * (xr[i][0].z * inv), bf_hi(gw.y) * (xr[i][0].w * inv));
+      xr[i][1] = make_float4(bf_lo(gw.z) * (xr[i][1].x * inv), bf_hi(gw.z) * (xr[i][1].y * inv),
+                             bf_lo(gw.w) * (xr[i][1].z * inv), bf_hi(gw.w) * (xr[i][1].w * inv));
+    }
+  }
+}
+
+// Rows [r0, r1) of W [rows, k]: wave w takes the row pairs r0 + 2 (w + NW j).
+// `pre` holds the wave's first pair, issued by the caller (before a
+// barrier); each pair's dot products are followed at once by the next pair's
+// loads into the same registers, so they are in flight during the epilogue
+// and the other waves' work (eight waves keep about 112 KB requested per CU
+// at the 7B shape, above the CU's intake rate times the memory latency).
+// epi(row, y_row, y_row+1) runs on every lane of the wave; rows past r1 are
+// skipped (their loads re-read row r1 - 1).
+template <int C, class Epi>
+__device__ __forceinline__ void wstream(u32x4 (&pre)[WRB][C], const uint16_t *W, int k, int r0, int r1,
+                                        const float4 (&xr)[C][2], int wave, int lane, Epi epi) {
+  if (r0 >= r1) return;
+  const int nb = (r1 - r0 + 2 * NW - 1) / (2 * NW);
+  for (int j = 0; j < nb; j++) {
+    const int ra = r0 + 2 * (wave + NW * j);
+    const float y0 = dotrow_x<C>(pre[0], xr, k, lane);
+    const float y1 = dotrow_x<C>(pre[1], xr, k, lane);
+    if (j + 1 < nb) wld<C>(pre, W, k, ra + 2 * NW, r1 - 1, lane);
+    if (ra < r1) epi(ra, y0, ra + 1 < r1 ? y1 : 0.f);
+  }
+}
+
+// gate/up tiles (a pair per wave) a workgroup owns; the rest are handed out
+// by ticket, so workgroups whose loads come in faster take more of them
+__host__ __device__ inline int wide_gu_static(int I) {
+  const int t = (3 * ((2 * I + 2 * NW - 1) / (2 * NW))) / (4 * NB);
+  return t > 1 ? t : 1;
+}
+
+// Rows of W [rows, k] in tiles of 2 NW rows, wave w taking rows 2w, 2w + 1 of
+// a tile: first this workgroup's tiles [t0, t0 + ns) (ns >= 1; `pre` holds
+// tile t0's pair; rows past `rows` are read clamped and skipped), then tile
+// dyn0 + i for each ticket base + i (i < ndyn)
+// that thread 0 draws from *tick. A ticket is drawn one tile ahead, so its
+// round trip overlaps a tile's loads; thread 0 posts the tile in tile_s
+// (two slots, alternating) for the other waves. Each workgroup draws exactly
+// one ticket past the last tile, so a pass advances the counter by
+// ndyn + NB. epi(row, y_row, y_row+1) runs on every lane of the wave.
+template <int C, class Epi>
+__device__ __forceinline__ void wstream_tiles(u32x4 (&pre)[WRB][C], const uint16_t *W, int k, int rows,
+                                              int t0, int ns, int dyn0, int ndyn, uint32_t *tick,
+                                              uint32_t base, int *tile_s, const float4 (&xr)[C][2],
+                                              int wave, int lane, int tid, Epi epi) {
+  int cur = t0, left = ns, slot = 0;
+  uint32_t tk = 0;
+  if (ns == 1 && tid == 0) tk = __hip_atomic_fetch_add(tick, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  for (;;) {
+    const int ra = cur * 2 * NW + 2 * wave;
+    const float y0 = dotrow_x<C>(pre[0], xr, k, lane);
+    const float y1 = dotrow_x<C>(pre[1], xr, k, lane);
+    int nxt;
+    if (left > 1) {
+      nxt = cur + 1;
+    } else {
+      if (tid == 0) {
+        const uint32_t i = tk - base;
+        tile_s[slot] = i < (uint32_t)ndyn ? dyn0 + (int)i : -1;
+      }
+      __syncthreads();
+      nxt = __builtin_amdgcn_readfirstlane(tile_s[slot]);
+      slot ^= 1;
+    }
+    if (nxt >= 0) {
+      wld<C>(pre, W, k, nxt * 2 * NW + 2 * wave, rows - 1, lane);
+      if (left <= 2 && tid == 0)
+        tk = __hip_atomic_fetch_add(tick, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (ra < rows) epi(ra, y0, ra + 1 < rows ? y1 : 0.f);
+    if (nxt < 0) break;
+    cur = nxt;
+    left--;
+  }
+}
+
+// first pair of the wave's rows in [r0, r1) into `pre`. Every load is issued:
+// an empty range reads at byte offset 2^31, past the descriptor's range
+// (zeros, no traffic), so the count of loads in flight after it does not
+// depend on the range and the compiler's waits on earlier loads stay exact.
+template <int C>
+__device__ __forceinline__ void wpre(u32x4 (&pre)[WRB][C], const uint16_t *W, int k, int r0, int r1,
+                                     int wave, int lane) {
+  const int nch = k >> 3;
+  const __amdgpu_buffer_rsrc_t rs = wrsrc(W);
+#pragma unroll
+  for (int rb = 0; rb < WRB; rb++) {
+    const int soff = r0 < r1 ? min(r0 + 2 * wave + rb, r1 - 1) * k * 2 : (int)0x80000000u;
+#pragma unroll
+    for (int i = 0; i < C; i++) {
+      const int c = min(lane + i * 64, nch - 1);
+      pre[rb][i] = __builtin_amdgcn_raw_buffer_load_b128(rs, c * 16, soff, 2);
+    }
+  }
+}
+
+// a down row pair: each thread's WDC chunks (tid + NT i) of rows `row`,
+// `row` + 1 (clamped to `last`, chunks clamped to the row)
+__device__ __forceinline__ void dld(u32x4 (&t)[2][WDC], const uint16_t *W, int k, int row, int last,
+                                    int tid) {
+  const int nch = k >> 3;
+  const __amdgpu_buffer_rsrc_t rs = wrsrc(W);
+#pragma unroll
+  for (int rb = 0; rb < 2; rb++) {
+    const int soff = min(row + rb, last) * k * 2;
+#pragma unroll
+    for (int i = 0; i < WDC; i++) {
+      const int c = min(tid + i * NT, nch - 1);
+      t[rb][i] = __builtin_amdgcn_raw_buffer_load_b128(rs, c * 16, soff, 2);
+    }
+  }
+}
+__device__ __forceinline__ float ddot(const u32x4 (&w)[WDC], const float4 (&hr)[WDC][2]) {
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < WDC; i++) {
+    const u32x4 q = w[i];
+    const float4 a = hr[i][0], b = hr[i][1];
+    s = fmaf(bf_lo(q.x), a.x, s);
+    s = fmaf(bf_hi(q.x), a.y, s);
+    s = fmaf(bf_lo(q.y), a.z, s);
+    s = fmaf(bf_hi(q.y), a.w, s);
+    s = fmaf(bf_lo(q.z), b.x, s);
+    s = fmaf(bf_hi(q.z), b.y, s);
+    s = fmaf(bf_lo(q.w), b.z, s);
+    s = fmaf(bf_hi(q.w), b.w, s);
+  }
+  return s;
+}
+
+template <int C, bool KB>
+__global__ void __launch_bounds__(NT) decode_wide_kernel(PersistArgs a) {
+  extern __shared__ float4 wsm4[];
+  float *xs = (float *)wsm4;   // [WXMAX] the phase's input vector
+  float *big = xs + WXMAX;     // attention staging / merge partials / argmax partials
+  uint16_t *gn_s = (uint16_t *)(big + wide_big_floats(a.d, a.max_seq));  // [WXMAX] next RMSNorm gains
+  // the layer table, copied to LDS once (a pointer read from global memory
+  // would be a vector load, and its wait would also wait for the weight loads
+  // in flight); layer(l) gives its pointers in scalar registers
+  PersistLayer *lay = (PersistLayer *)(gn_s + WXMAX);
+  __shared__ float xl[WMR];    // this workgroup's down rows of the residual stream
+  __shared__ float xol[WOR];   // the residual at its o rows
+  __shared__ float red[NW][WMR];
+  __shared__ int fail_s;
+  __shared__ uint32_t tok_s;
+  __shared__ float2 best_s[NW];
+  __shared__ float qb_s[WQP];      // this workgroup's QKV biases, loaded ahead
+  __shared__ float2 qcs_s[WQP / 2];  // RoPE (cos, sin) of its pairs at the step's position
+  __shared__ int last_s;
+  __shared__ int tile_s[2];
+
+  // tid and lane are re-derived at the top of every step and layer (see
+  // opaque), so per-lane addresses are not hoisted out of the loops and held
+  // in registers (spilled) for the whole launch
+  int tid = threadIdx.x, lane = tid & 63;
+  const int wg = blockIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int H = a.H, I = a.I, V = a.V, d = a.d, nq = a.nq, nkv = a.nkv;
+  const int half = d >> 1, gq = nq / nkv, qdim = nq * d, kvdim = nkv * d;
+  const int qkv_rows = qdim + 2 * kvdim;
+  const uint32_t TPS = (uint32_t)a.L * kTPL + 2;
+  const int nchmax = (a.max_seq + AC - 1) / AC;
+  const WideBufs B = wide_bufs(a.wide, H, I, nq, d, a.max_seq, nullptr);
+  // ownership: QKV row pairs, residual rows (o and down), gate/up row pairs,
+  // head rows
+  const int qper = 2 * ((qkv_rows + 2 * NB - 1) / (2 * NB));
+  const int q0 = min(wg * qper, qkv_rows), q1 = min(q0 + qper, qkv_rows);
+  const int xper = (H + NB - 1) / NB;
+  const int x0 = min(wg * xper, H), x1 = min(x0 + xper, H), nx = x1 - x0;
+  // o rows: when the attention items fit in the first quarter of the grid,
+  // those workgroups hold none, so nothing but their item waits on their loads
+  const int ow0 = wide_item_wgs(nkv, nchmax);
+  const int oper = (H + (NB - ow0) - 1) / (NB - ow0);
+  const int o0r = wg < ow0 ? H : min((wg - ow0) * oper, H), o1r = min(o0r + oper, H);
+  // gate/up: static tiles of 2 NW rows, then tiles by ticket
+  const int gns = wide_gu_static(I), gtiles = (2 * I + 2 * NW - 1) / (2 * NW);
+  const int gdyn0 = NB * gns, gndyn = max(gtiles - gdyn0, 0);
+  const int g0 = min(wg * gns * 2 * NW, 2 * I), g1 = min(g0 + gns * 2 * NW, 2 * I);
+  const int vper = (V + NB - 1) / NB;
+  const int v0 = min(wg * vper, V), v1 = min(v0 + vper, V);
+  // biases and RoPE factors of this workgroup's QKV rows for layer l at
+  // position p, into LDS ahead of the phase (the epilogue then loads nothing)
+  auto gains_ld = [&](const uint16_t *g) {
+    return __builtin_amdgcn_raw_buffer_load_b128(gsrc(g), tid < (H >> 3) ? tid * 16 : 0x7fffffff, 0, 0);
+  };
+  auto layer = [&](int l) {
+    const PersistLayer &q = lay[l];
+    PersistLayer p;
+    p.ln1 = uni(q.ln1);
+    p.wqkv = uni(q.wqkv);
+    p.wo = uni(q.wo);
+    p.ln2 = uni(q.ln2);
+    p.wgu = uni(q.wgu);
+    p.wd = uni(q.wd);
+    p.bqkv = uni(q.bqkv);
+    p.wdp = nullptr;
+    return p;
+  };
+  struct Consts {
+    float b;
+    float2 cs;
+    u32x4 g;
+  };
+  // loads of layer l's constants at position p: this thread's QKV bias and
+  // RoPE pair, and its 8 RMSNorm gains (ln1); consts_st puts them in LDS, so
+  // the loads can go out ahead of a phase's weight loads
+  auto consts_ld = [&](int l, uint32_t p) {
+    // buffer loads: an offset past the range (2^31) reads 0 and fetches nothing
+    Consts c;
+    const int r = q0 + 2 * tid;
+    const int ib = tid < q1 - q0 ? (q0 + tid) * 4 : 0x7fffffff;
+    const int ir = tid < (q1 - q0) / 2 && r < qdim + kvdim
+                       ? (int)(((size_t)p * half + (((r < qdim ? r : r - qdim) >> 1) % half)) * 8)
+                       : 0x7fffffff;
+    c.b = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(gsrc(uni(lay[l].bqkv)), ib, 0, 0));
+    const u32x2 cs = __builtin_amdgcn_raw_buffer_load_b64(gsrc(a.rope), ir, 0, 0);
+    c.cs = ir == 0x7fffffff ? make_float2(1.f, 0.f) : make_float2(__uint_as_float(cs.x), __uint_as_float(cs.y));
+    c.g = gains_ld(uni(lay[l].ln1));
+    return c;
+  };
+  auto consts_st = [&](const Consts &c) {
+    if (tid < q1 - q0) qb_s[tid] = c.b;
+    if (tid < (q1 - q0) / 2) qcs_s[tid] = c.cs;
+    if (tid < (H >> 3)) *(u32x4 *)(gn_s + tid * 8) = c.g;
+  };
+
+  auto gains_st = [&](const u32x4 &g) {
+    if (tid < (H >> 3)) *(u32x4 *)(gn_s + tid * 8) = g;
+  };
+  for (int i = tid; i < a.L * (int)(sizeof(PersistLayer) / 8); i += NT)
+    ((uint64_t *)lay)[i] = ((const uint64_t *)a.layers)[i];
+  if (tid == 0) fail_s = 0;
+  if (tid < WMR) xl[tid] = 0.f;
+  // the ticket counter starts at 0; the first barrier orders this store
+  // before every draw
+  if (wg == 0 && tid == 0) __hip_atomic_store(B.tick, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+
+  u32x4 pre[WRB][C];          // the next wave-row phase's first pair
+  u32x4 dpre[2][WDC];         // the down phase's first pair
+  wpre<C>(pre, uni(lay[0].wqkv), H, q0, q1, wave, lane);
+
+  for (uint32_t s = 0; s < a.steps; s++) {
+    tid = opaque(tid);
+    lane = tid & 63;
+    const uint32_t pos = a.pos0 + s;
+    const int seq = (int)pos + 1;
+    const uint32_t tstep = a.tag_base + s * TPS;
+
+    // ---- token: argmax of the previous logits; embedding row -----------------
+    {
+      float bv = -INFINITY;
+      uint32_t bi = 0xffffffffu;
+      if (s == 0) {
+        for (int i = tid; i < a.nparts_in; i += NT) {
+          const float2 p = a.part_in[i];
+          if (beats(p.x, __float_as_uint(p.y), bv, bi)) {
+            bv = p.x;
+            bi = __float_as_uint(p.y);
+          }
+        }
+      } else if (tid < NB) {
+        const __amdgpu_buffer_rsrc_t rs = crsrc(B.arg);
+        bv = cld(rs, 2 * tid);
+        bi = __float_as_uint(cld(rs, 2 * tid + 1));
+      }
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(bv, o, 64);
+        const uint32_t oi = __shfl_xor(bi, o, 64);
+        if (beats(ov, oi, bv, bi)) {
+          bv = ov;
+          bi = oi;
+        }
+      }
+      if (lane == 0) best_s[wave] = make_float2(bv, __uint_as_float(bi));
+      __syncthreads();
+      if (tid == 0) {
+        float2 b = best_s[0];
+        for (int w = 1; w < NW; w++)
+          if (beats(best_s[w].x, __float_as_uint(best_s[w].y), b.x, __float_as_uint(b.y))) b = best_s[w];
+        const uint32_t idx = __float_as_uint(b.y);
+        const uint32_t best = idx < (uint32_t)V ? idx : 0u;  // no candidate (all NaN / -inf) -> 0
+        if (wg == 0) a.out_ids[s] = best;
+        tok_s = a.force ? a.force[s] : best;  // teacher forcing feeds the given id
+        if (wg == 0 && s + 1 == a.steps) a.state[1] = tok_s;
+      }
+      __syncthreads();
+      const uint16_t *erow = a.embed + (size_t)tok_s * H;
+      for (int j = tid; j < H; j += NT) xs[j] = bf16f(erow[j]);
+      if (tid < nx) xl[tid] = bf16f(erow[x0 + tid]);
+      consts_st(consts_ld(0, pos));
+      __syncthreads();
+    }
+
+    for (int l = 0; l < a.L; l++) {
+      tid = opaque(tid);
+      lane = tid & 63;
+      const PersistLayer Ly = layer(l);
+      const uint32_t T = tstep + (uint32_t)l * kTPL;
+      constexpr int kvb = KB ? 2 : 4;
+      uint8_t *kc = (uint8_t *)a.kc + (size_t)l * a.layer_kv * kvb;
+      uint8_t *vc = (uint8_t *)a.vc + (size_t)l * a.layer_kv * kvb;
+
+      // ---- QKV + bias + RoPE + KV store ----------------------------------------
+      {
+        if (l > 0) cload_vec(xs, B.x, H, tid);
+        __syncthreads();
+        if (tid < o1r - o0r) xol[tid] = xs[o0r + tid];
+        float4 xr[C][2];
+        wnorm<C>(xr, xs, gn_s, H, a.eps, lane);
+        wstream<C>(pre, Ly.wqkv, H, q0, q1, xr, wave, lane, [&](int r, float y0, float y1) {
+          if (lane != 0) return;
+          const float b0 = y0 + qb_s[r - q0], b1 = y1 + qb_s[r - q0 + 1];
+          if (r < qdim + kvdim) {
+            const bool is_q = r < qdim;
+            const int qu = (is_q ? r : r - qdim) >> 1, head = qu / half, p = qu - head * half;
+            const float2 cs = qcs_s[(r - q0) >> 1];
+            const float o0 = b0 * cs.x - b1 * cs.y, o1 = b1 * cs.x + b0 * cs.y;
+            if (is_q) {
+              cstore(B.q + head * d + p, o0);
+              cstore(B.q + head * d + p + half, o1);
+            } else {
+              const size_t base = ((size_t)head * a.max_seq + pos) * d;
+              kvstore<KB>(kc, base + p, o0);
+              kvstore<KB>(kc, base + p + half, o1);
+            }
+          } else {
+            const int rr = r - qdim - kvdim, head = rr / d, j = rr - head * d;
+            const size_t base = ((size_t)head * a.max_seq + pos) * d + j;
+            kvstore<KB>(vc, base, b0);
+            kvstore<KB>(vc, base + 1, b1);
+          }
+        });
+      }
+
+      // ---- attention partials for (kv head, chunk) items, merged by the last
+      // item of each kv group -------------------------------------------------
+      // Thread i = tid + u NT holds columns [4 j4, 4 j4 + 4) of position
+      // t = i / dq of the chunk (dq = d / 4 lanes per position), K in
+      // registers and V staged in LDS; a score is a dq-lane segmented sum; wave
+      // h then takes q head h (softmax over the chunk, the V sum). The first
+      // item's cached rows (positions before this step's) load ahead of the
+      // barrier; this step's row (written by the QKV phase) after it.
+      const int nch = (seq + AC - 1) / AC;
+      const int dq = d >> 2, j4 = tid & (dq - 1);
+      const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+          kc, (short)0, (int)(a.layer_kv * kvb), 0x00020000);
+      const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+          vc, (short)0, (int)(a.layer_kv * kvb), 0x00020000);
+      u32x4 kr[KV4], vr[KV4];
+      // rows t in [tmin, tmax) of item it into kr / vr
+      auto item_rows = [&](int it, int tmin, int tmax) {
+        const int g = it % nkv, t0 = (it / nkv) * AC;
+#pragma unroll
+        for (int u = 0; u < KV4; u++) {
+          const int t = (tid + u * NT) / dq;
+          if (t >= tmin && t < tmax) {
+            const uint32_t off = (uint32_t)((((size_t)g * a.max_seq + t0 + t) * d + j4 * 4) * kvb);
+            if (KB) {
+              const u32x2 k2 = __builtin_amdgcn_raw_buffer_load_b64(rk, off, 0, 16);
+              const u32x2 v2 = __builtin_amdgcn_raw_buffer_load_b64(rv, off, 0, 16);
+              kr[u] = (u32x4){k2.x << 16, k2.x & 0xffff0000u, k2.y << 16, k2.y & 0xffff0000u};
+              vr[u] = (u32x4){v2.x << 16, v2.x & 0xffff0000u, v2.y << 16, v2.y & 0xffff0000u};
+            } else {
+              kr[u] = __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 16);
+              vr[u] = __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, 16);
+            }
+          }
+        }
+      };
+      // positions of item it: n; cached ones: nold (the last chunk ends at pos)
+      auto item_n = [&](int it) { return min(AC, seq - (it / nkv) * AC); };
+      auto item_nold = [&](int it) { return (it / nkv) == nch - 1 ? item_n(it) - 1 : item_n(it); };
+#pragma unroll
+      for (int u = 0; u < KV4; u++) {
+        const u32x4 zero = {0u, 0u, 0u, 0u};
+        kr[u] = zero;
+        vr[u] = zero;
+      }
+      wide_barrier(a, T + W_QKV, &fail_s, [&] {
+        if (wg < nkv * nch) item_rows(wg, 0, item_nold(wg));
+      });
+
+      for (int it = wg; it < nkv * nch; it += NB) {
+        const int g = it % nkv, c = it / nkv;
+        const int n = item_n(it);
+        float *q_s = big;                 // [gq][d]
+        float *v_s = q_s + WMAXQ * MAXD;  // [AC][d]
+        float *p_s = v_s + AC * MAXD;     // [gq][AC] scaled scores -> weights
+        if (it == wg) {
+          item_rows(it, item_nold(it), n);
+        } else {
+#pragma unroll
+          for (int u = 0; u < KV4; u++) {
+            const u32x4 zero = {0u, 0u, 0u, 0u};
+            kr[u] = zero;
+            vr[u] = zero;
+          }
+          item_rows(it, 0, n);
+        }
+        {
+          const __amdgpu_buffer_rsrc_t rq = crsrc(B.q);
+          float qv[2];
+#pragma unroll
+          for (int u = 0; u < 2; u++) {
+            const int i = tid + u * NT;
+            qv[u] = cld(rq, i < gq * d ? g * gq * d + i : 0);
+          }
+#pragma unroll
+          for (int u = 0; u < 2; u++) {
+            const int i = tid + u * NT;
+            if (i < gq * d) q_s[(i / d) * MAXD + (i % d)] = qv[u];
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < KV4; u++) {
+          const int t = (tid + u * NT) / dq;
+          if (t < n)
+            *(float4 *)(v_s + t * MAXD + j4 * 4) =
+                make_float4(__uint_as_float(vr[u].x), __uint_as_float(vr[u].y),
+                            __uint_as_float(vr[u].z), __uint_as_float(vr[u].w));
+        }
+        __syncthreads();
+        const float scale = 1.0f / sqrtf((float)d);
+#pragma unroll
+        for (int u = 0; u < KV4; u++) {
+          const int t = (tid + u * NT) / dq;
+          const float4 k4 = make_float4(__uint_as_float(kr[u].x), __uint_as_float(kr[u].y),
+                                        __uint_as_float(kr[u].z), __uint_as_float(kr[u].w));
+#pragma unroll
+          for (int h = 0; h < WMAXQ; h++) {
+            if (h >= gq) break;
+            const float4 q4 = *(const float4 *)(q_s + h * MAXD + j4 * 4);
+            float sc = q4.x * k4.x;
+            sc = fmaf(q4.y, k4.y, sc);
+            sc = fmaf(q4.z, k4.z, sc);
+            sc = fmaf(q4.w, k4.w, sc);
+            sc = seg_sum(sc, dq);
+            if (t < n && seg_leader(lane, dq)) p_s[h * AC + t] = sc * scale;
+          }
+        }
+        __syncthreads();
+        if (wave < gq) {
+          const int h = wave;
+          const float sc = lane < n ? p_s[h * AC + lane] : -INFINITY;
+          const float mx = wave_max(sc);
+          const float e = lane < n ? expf(sc - mx) : 0.f;
+          const float lsum = wave_sum(e);
+          if (lane < AC) p_s[h * AC + lane] = e;
+          const int j0 = lane & (d - 1), j1 = (lane + 64) & (d - 1);
+          float o0 = 0.f, o1 = 0.f;
+#pragma unroll
+          for (int t4 = 0; t4 < AC; t4 += 4) {
+            if (t4 < n) {
+              const float4 e4 = *(const float4 *)(p_s + h * AC + t4);
+              const float ev[4] = {e4.x, e4.y, e4.z, e4.w};
+#pragma unroll
+              for (int k = 0; k < 4; k++) {
+                // rows past n hold stale LDS: masked, not just weighted by 0
+                const float *vt = v_s + (t4 + k) * MAXD;
+                const bool in = t4 + k < n;
+                o0 = fmaf(ev[k], in ? vt[j0] : 0.f, o0);
+                o1 = fmaf(ev[k], in ? vt[j1] : 0.f, o1);
+              }
+            }
+          }
+          float *dst = B.part + ((size_t)(g * gq + h) * nchmax + c) * (d + 2);
+          if (lane < d) cstore(dst + lane, o0);
+          if (lane + 64 < d) cstore(dst + lane + 64, o1);
+          if (lane == 0) {
+            cstore(dst + d, mx);
+            cstore(dst + d + 1, lsum);
+          }
+        }
+        // count the item in once its partial stores have completed; the
+        // group's last item merges the group's heads, wave h taking head h:
+        // att = sum_c e^(m_c - M) o_c / sum_c e^(m_c - M) l_c, chunks in order
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (tid == 0)
+          last_s = __hip_atomic_fetch_add(&B.cnt[g], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                   nch - 1;
+        __syncthreads();
+        if (last_s) {
+          for (int h = wave; h < gq; h += NW) {
+            const int hh = g * gq + h, dd = d + 2;
+            const __amdgpu_buffer_rsrc_t rp = crsrc(B.part + (size_t)hh * nchmax * dd);
+            const int ja = lane < d ? lane : 0, jb = lane + 64 < d ? lane + 64 : 0;
+            // a batch of 8 chunks' outputs per round trip, the first one
+            // issued with the (m, l) pairs; chunks past nch read at byte
+            // offset 2^31 (zeros, no traffic) and carry weight 0
+            float v0[8], v1[8];
+            auto batch = [&](int cb) {
+#pragma unroll
+              for (int u = 0; u < 8; u++) {
+                const int cc = cb + u;
+                v0[u] = cldb(rp, cc < nch ? (cc * dd + ja) * 4 : (int)0x80000000u);
+                v1[u] = cldb(rp, cc < nch ? (cc * dd + jb) * 4 : (int)0x80000000u);
+              }
+            };
+            const float m = lane < nch ? cld(rp, lane * dd + d) : -INFINITY;
+            const float lw = lane < nch ? cld(rp, lane * dd + d + 1) : 0.f;
+            batch(0);
+            const float mx = wave_max(m);
+            const float e = lane < nch ? expf(m - mx) : 0.f;
+            const float inv = 1.0f / wave_sum(e * lw);
+            float acc0 = 0.f, acc1 = 0.f;
+            for (int cb = 0;;) {
+#pragma unroll
+              for (int u = 0; u < 8; u++) {
+                const float ec = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), cb + u));
+                acc0 = fmaf(ec, v0[u], acc0);
+                acc1 = fmaf(ec, v1[u], acc1);
+              }
+              cb += 8;
+              if (cb >= nch) break;
+              batch(cb);
+            }
+            if (lane < d) cstore(B.att + hh * d + lane, acc0 * inv);
+            if (lane + 64 < d) cstore(B.att + hh * d + lane + 64, acc1 * inv);
+          }
+          if (tid == 0) __hip_atomic_store(&B.cnt[g], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __syncthreads();
+      }
+      // the o rows' loads (a workgroup with none takes its gate/up loads):
+      // `pre` is then written on every path here, so it holds nothing live
+      // through the attention items
+      wide_barrier(a, T + W_ATT, &fail_s, [&] {
+        const u32x4 g = gains_ld(Ly.ln2);
+        asm volatile("" ::: "memory");  // the gains' load goes out first
+        const bool has_o = o0r < o1r;
+        wpre<C>(pre, has_o ? Ly.wo : Ly.wgu, has_o ? qdim : H, has_o ? o0r : g0, has_o ? o1r : g1, wave,
+                lane);
+        gains_st(g);
+      });
+
+      // ---- o projection + residual ------------------------------------------
+      {
+        cload_vec(xs, B.att, qdim, tid);
+        __syncthreads();
+        float4 xr[C][2];
+        load_x<C>(xr, xs, qdim, lane);
+        wstream<C>(pre, Ly.wo, qdim, o0r, o1r, xr, wave, lane, [&](int r, float y0, float y1) {
+          if (lane != 0) return;
+          cstore(B.xo + r, xol[r - o0r] + y0);
+          if (r + 1 < o1r) cstore(B.xo + r + 1, xol[r + 1 - o0r] + y1);
+        });
+      }
+      wide_barrier(a, T + W_XO, &fail_s, [&] {
+        if (o0r < o1r) wpre<C>(pre, Ly.wgu, H, g0, g1, wave, lane);
+      });
+
+      // ---- RMSNorm + gate/up + SwiGLU -------------------------------------------
+      {
+        cload_vec(xs, B.xo, H, tid);
+        __syncthreads();
+        if (tid < nx) xl[tid] = xs[x0 + tid];
+        float4 xr[C][2];
+        wnorm<C>(xr, xs, gn_s, H, a.eps, lane);
+        const uint32_t tbase = (s * (uint32_t)a.L + (uint32_t)l) * (uint32_t)(gndyn + NB);
+        wstream_tiles<C>(pre, Ly.wgu, H, 2 * I, wg * gns, gns, gdyn0, gndyn, B.tick, tbase, tile_s, xr,
+                         wave, lane, tid, [&](int r, float y0, float y1) {
+                           if (lane == 0) cstore(B.h + (r >> 1), silu(y0) * y1);
+                         });
+      }
+      wide_barrier(a, T + W_H, &fail_s, [&] {
+        if (nx > 0) dld(dpre, Ly.wd, I, x0, x1 - 1, tid);
+      });
+
+      // ---- down + residual: whole-workgroup rows, h slice in registers ---------
+      {
+        const int nchi = I >> 3;
+        float4 hr[WDC][2];
+        {
+          const __amdgpu_buffer_rsrc_t rh = crsrc(B.h);
+#pragma unroll
+          for (int i = 0; i < WDC; i++) {
+            const int c = tid + i * NT;
+            const int cc = c < nchi ? c : 0;
+            const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+            const u32x4 p = __builtin_amdgcn_raw_buffer_load_b128(rh, cc * 32, 0, 16);
+            const u32x4 q = __builtin_amdgcn_raw_buffer_load_b128(rh, cc * 32 + 16, 0, 16);
+            hr[i][0] = c < nchi ? make_float4(__uint_as_float(p.x), __uint_as_float(p.y),
+                                              __uint_as_float(p.z), __uint_as_float(p.w)) : z;
+            hr[i][1] = c < nchi ? make_float4(__uint_as_float(q.x), __uint_as_float(q.y),
+                                              __uint_as_float(q.z), __uint_as_float(q.w)) : z;
+          }
+        }
+        // row pair p from set A (even p, first one issued before the
+        // barrier) or B (odd p), the next pair's loads issued before the
+        // current pair's dot products; a compiler memory barrier after each
+        // pair keeps later pairs' loads from being hoisted (which would hold
+        // every pair in registers at once)
+        u32x4 dn[2][WDC];
+        auto pair = [&](int r, u32x4 (&cur)[2][WDC], u32x4 (&nxt)[2][WDC]) {
+          if (r + 2 < nx) dld(nxt, Ly.wd, I, x0 + r + 2, x1 - 1, tid);
+          const float y0 = wave_sum(ddot(cur[0], hr)), y1 = wave_sum(ddot(cur[1], hr));
+          if (lane == 0) {
+            red[wave][r] = y0;
+            if (r + 1 < nx) red[wave][r + 1] = y1;
+          }
+          asm volatile("" ::: "memory");
+        };
+#pragma unroll
+        for (int r = 0; r < WMR; r += 4) {
+          if (r < nx) pair(r, dpre, dn);
+          if (r + 2 < nx) pair(r + 2, dn, dpre);
+        }
+        __syncthreads();
+        if (tid < nx) {
+          float sum = 0.f;
+#pragma unroll
+          for (int w = 0; w < NW; w++) sum += red[w][tid];
+          const float v = xl[tid] + sum;
+          xl[tid] = v;
+          cstore(B.x + x0 + tid, v);
+        }
+      }
+      wide_barrier(a, T + W_X, &fail_s, [&] {
+        if (l + 1 < a.L) {
+          const Consts c = consts_ld(l + 1, pos);
+          asm volatile("" ::: "memory");  // the constants' loads go out first
+          wpre<C>(pre, uni(lay[l + 1].wqkv), H, q0, q1, wave, lane);
+          consts_st(c);
+        } else
+          wpre<C>(pre, a.head, H, v0, v1, wave, lane);
+      });
+    }
+
+    // ---- final norm + head + argmax partial (tag tstep + 6 L) --------------------
+    const uint32_t TH = tstep + (uint32_t)a.L * kTPL;
+    {
+      cload_vec(xs, B.x, H, tid);
+      __syncthreads();
+      float4 xr[C][2];
+      wnorm<C>(xr, xs, a.final_norm, H, a.eps, lane);
+      if (wg == 0 && wave == 0) {
+#pragma unroll
+        for (int i = 0; i < C; i++) {
+          const int c = lane + i * 64;
+          if (c < (H >> 3)) {
+            *(float4 *)(a.normed + c * 8) = xr[i][0];
+            *(float4 *)(a.normed + c * 8 + 4) = xr[i][1];
+          }
+        }
+      }
+      float bv = -INFINITY;
+      uint32_t bi = 0xffffffffu;
+      wstream<C>(pre, a.head, H, v0, v1, xr, wave, lane, [&](int r, float y0, float y1) {
+        if (lane == 0) a.logits[r] = y0;
+        if (beats(y0, (uint32_t)r, bv, bi)) {
+          bv = y0;
+          bi = (uint32_t)r;
+        }
+        if (r + 1 < v1) {
+          if (lane == 0) a.logits[r + 1] = y1;
+          if (beats(y1, (uint32_t)(r + 1), bv, bi)) {
+            bv = y1;
+            bi = (uint32_t)(r + 1);
+          }
+        }
+      });
+      if (lane == 0) best_s[wave] = make_float2(bv, __uint_as_float(bi));
+      __syncthreads();
+      if (tid == 0) {
+        float2 b = best_s[0];
+        for (int w = 1; w < NW; w++)
+          if (beats(best_s[w].x, __float_as_uint(best_s[w].y), b.x, __float_as_uint(b.y))) b = best_s[w];
+        cstore(B.arg + 2 * wg, b.x);
+        cstore(B.arg + 2 * wg + 1, b.y);
+      }
+    }
+    wide_barrier(a, TH, &fail_s, [&] {
+      if (s + 1 < a.steps) wpre<C>(pre, uni(lay[0].wqkv), H, q0, q1, wave, lane);
+    });
+  }
+
+  // ---- hand the state back to the per-kernel path ---------------------------
+  if (tid < nx) a.x_out[x0 + tid] = xl[tid];
+  if (wg == 0) {
+    float bv = -INFINITY;
+    uint32_t bi = 0xffffffffu;
+    if (tid < NB) {
+      const __amdgpu_buffer_rsrc_t rs = crsrc(B.arg);
+      bv = cld(rs, 2 * tid);
+      bi = __float_as_uint(cld(rs, 2 * tid + 1));
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      const float ov = __shfl_xor(bv, o, 64);
+      const uint32_t oi = __shfl_xor(bi, o, 64);
+      if (beats(ov, oi, bv, bi)) {
+        bv = ov;
+        bi = oi;
+      }
+    }
+    if (lane == 0) best_s[wave] = make_float2(bv, __uint_as_float(bi));
+    __syncthreads();
+    if (tid == 0) {
+      float2 b = best_s[0];
+      for (int w = 1; w < NW; w++)
+        if (beats(best_s[w].x, __float_as_uint(best_s[w].y), b.x, __float_as_uint(b.y))) b = best_s[w];
+      best_s[0] = b;
+      a.state[0] = a.pos0 + a.steps;
+      a.state[2] = a.steps;
+    }
+    __syncthreads();
+    const float2 none = make_float2(-INFINITY, __uint_as_float(0xffffffffu));
+    for (int i = tid; i < a.part_cap; i += NT) a.part_out[i] = i == 0 ? best_s[0] : none;
+  }
+}
+
 }  // namespace
 
 int persist_grid() { return NB; }
@@ -1257,6 +2147,69 @@ hipError_t launch_decode_persistent(const PersistArgs &a, hipStream_t s) {
   }
   void *params[] = {&args};
   return hipLaunchCooperativeKernel(fn, dim3(NB), dim3(NT), params, (unsigned)smem, s);
+}
+
+
+// ---- streamed cooperative decode: support and launch ---------------------------
+static size_t wide_lds_bytes(int d, int max_seq) {
+  return (WXMAX + wide_big_floats(d, max_seq) + WXMAX / 2) * sizeof(float) + WLMAX * sizeof(PersistLayer);
+}
+
+bool wide_supported(int H, int I, int qdim, int d, int gq, int max_seq) {
+  // 8-column chunks; rows of at most 64 x 8 x 7 columns held in a wave,
+  // down rows of at most 512 x 8 x WDC columns held in a workgroup
+  if (H % 8 || I % 8 || qdim % 8) return false;
+  if (H > 64 * 8 * 7 || qdim > 64 * 8 * 7 || I > NT * 8 * WDC || H > WXMAX) return false;
+  if ((H + NB - 1) / NB > WMR) return false;
+  // the attention items sum a score over d / 4 lanes: d in {32, 64, 128};
+  // the merge takes a head's chunks one per lane; QKV rows per workgroup
+  if ((d & (d - 1)) || d < 32 || d > MAXD || gq > WMAXQ) return false;
+  if ((max_seq + AC - 1) / AC > WMCH) return false;
+  const int qkv_rows = qdim + 2 * (qdim / gq);
+  if (2 * ((qkv_rows + 2 * NB - 1) / (2 * NB)) > WQP || qdim / gq / d > WMAXQ * 64) return false;
+  const int ow0 = wide_item_wgs(qdim / gq / d, (max_seq + AC - 1) / AC);
+  if ((H + (NB - ow0) - 1) / (NB - ow0) > WOR) return false;
+  return wide_lds_bytes(d, max_seq) <= kMaxLds - 2048;  // room for the static LDS
+}
+
+size_t wide_buffer_floats(int H, int I, int nq, int d, int max_seq) {
+  size_t total = 0;
+  (void)wide_bufs(nullptr, H, I, nq, d, max_seq, &total);
+  return total;
+}
+
+bool wide_device_ok(const PersistArgs &a) {
+  if (!wide_supported(a.H, a.I, a.nq * a.d, a.d, a.nq / a.nkv, a.max_seq) || a.L > WLMAX) return false;
+  int dev = 0, coop = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return false;
+  if (hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev) != hipSuccess) return false;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return false;
+  return coop != 0 && cus >= NB;
+}
+
+hipError_t launch_decode_wide(const PersistArgs &a, hipStream_t s) {
+  if (!wide_supported(a.H, a.I, a.nq * a.d, a.d, a.nq / a.nkv, a.max_seq)) return hipErrorInvalidValue;
+  if (a.steps == 0) return hipSuccess;
+  if (a.pos0 + a.steps > (uint32_t)a.max_seq) return hipErrorInvalidValue;
+  const size_t smem = wide_lds_bytes(a.d, a.max_seq);
+  const bool narrow = a.H <= 64 * 8 * 3 && a.nq * a.d <= 64 * 8 * 3;
+  const bool kb = a.kv_bf16 != 0;
+  const void *const fns[4] = {(const void *)decode_wide_kernel<7, false>,
+                              (const void *)decode_wide_kernel<7, true>,
+                              (const void *)decode_wide_kernel<3, false>,
+                              (const void *)decode_wide_kernel<3, true>};
+  const int which = 2 * narrow + kb;
+  // the dynamic LDS this launch needs (the kernel's static LDS comes on top
+  // of it, within the 160 KB a workgroup can hold)
+  static size_t attr_set[4] = {0, 0, 0, 0};
+  if (attr_set[which] < smem) {
+    hipError_t e = hipFuncSetAttribute(fns[which], hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+    if (e != hipSuccess) return e;
+    attr_set[which] = smem;
+  }
+  PersistArgs args = a;
+  void *params[] = {&args};
+  return hipLaunchCooperativeKernel(fns[which], dim3(NB), dim3(NT), params, (unsigned)smem, s);
 }
 
 }  // namespace myos

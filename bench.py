@@ -237,7 +237,8 @@ def main():
     ap.add_argument("--no-arena", action="store_true")
     ap.add_argument("--kernel-reps", type=int, default=20)
     ap.add_argument("--no-graph", action="store_true")
-    ap.add_argument("--decode-path", choices=["auto", "kernels", "persistent"], default="auto")
+    ap.add_argument("--decode-path", choices=["auto", "kernels", "persistent", "streamed"],
+                    default="auto")
     ap.add_argument("--no-gemv-microbench", action="store_true")
     ap.add_argument("--shape", choices=["qwen2.5-1.5b", "qwen2.5-7b"], default="qwen2.5-1.5b",
                     help="model shape (the headline metric is quoted on qwen2.5-1.5b)")
@@ -292,8 +293,10 @@ def main():
     if args.no_graph:
         m.set_graph(False)
     m.set_decode_mode({"auto": myos.DECODE_AUTO, "kernels": myos.DECODE_KERNELS,
-                       "persistent": myos.DECODE_PERSISTENT}[args.decode_path])
-    path_name = "persistent" if m.decode_path() == myos.DECODE_PERSISTENT else "kernels"
+                       "persistent": myos.DECODE_PERSISTENT,
+                       "streamed": myos.DECODE_STREAMED}[args.decode_path])
+    path_name = {myos.DECODE_PERSISTENT: "persistent", myos.DECODE_STREAMED: "streamed",
+                 myos.DECODE_KERNELS: "kernels"}[m.decode_path()]
     log(f"decode path: {path_name}")
 
     def step():
@@ -352,6 +355,7 @@ def main():
         o_lg = ref["final_logits"]
         rel = {}
         for name, mode in (("persistent", myos.DECODE_PERSISTENT),
+                           ("streamed", myos.DECODE_STREAMED),
                            ("kernels", myos.DECODE_KERNELS)):
             try:
                 m.set_decode_mode(mode)
@@ -383,17 +387,17 @@ def main():
     # the committed traffic figures are for the 1.5B shape with the f32 cache
     tinfo = (json.load(open(tpath))
              if os.path.exists(tpath) and kv == myos.KV_F32 and not is7b else {})
-    if path_name == "persistent":
+    if path_name in ("persistent", "streamed"):
         launch_bytes = b_tok * args.decode
         launch_s = dd / args.steps * 1e-3
         achieved = launch_bytes / launch_s
         traffic, tsrc = None, None
-        t = tinfo.get("persistent_launch")
+        t = tinfo.get("persistent_launch") if path_name == "persistent" else None
         if t and t.get("decode_steps") == args.decode and t.get("prompt_ids") == args.prompt:
             traffic, tsrc = t["traffic_bytes"], t["source"]
         roofline = {"bound": "hbm",
-                    "kernel": f"decode_persistent_kernel (one launch: {args.decode} greedy "
-                              f"decode steps)",
+                    "kernel": f"{'decode_persistent_kernel' if path_name == 'persistent' else 'decode_wide_kernel'} "
+                              f"(one launch: {args.decode} greedy decode steps)",
                     "achieved": round(achieved / 1e9, 1), "peak": HBM_PEAK / 1e9,
                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK, 4), "traffic": traffic,
                     "traffic_source": tsrc and f"{tsrc}: rocprofv3 --pmc FETCH_SIZE and "

@@ -207,10 +207,17 @@ int myos_set_graph(myos_model *m, int enabled);
  * PERSISTENT when the model allows it (f32 or bf16 cache, hidden and q_dim <=
  * 1536 and multiples of 32 and 8, intermediate <= 9216, head_dim 32, 64 or
  * 128, at most 8 q heads per kv head, and the kernel's LDS budget) and the
- * device has >= 256 CUs with cooperative launch. Setting PERSISTENT where it is not
- * available returns MYOS_E_SHAPE. myos_decode_path returns the path the next
- * call takes. */
-enum { MYOS_DECODE_AUTO = 0, MYOS_DECODE_KERNELS = 1, MYOS_DECODE_PERSISTENT = 2 };
+ * device has >= 256 CUs with cooperative launch. Where that kernel does not
+ * fit, AUTO and PERSISTENT take STREAMED: a cooperative kernel that streams
+ * each phase's weight rows from HBM and meets at device-wide barriers (hidden
+ * and q_dim <= 3584, intermediate <= 20480, head_dim 32, 64 or 128, at most 8
+ * q heads per kv head, max_seq <= 2048, at most 128 layers; the 7B shape). STREAMED can also be asked for on any
+ * model it fits. Setting PERSISTENT or STREAMED where neither is available
+ * returns MYOS_E_SHAPE. myos_decode_path returns the path the next call takes
+ * (KERNELS, PERSISTENT for the register-resident kernel, or STREAMED); the
+ * decode trace records the register-resident kernel only. */
+enum { MYOS_DECODE_AUTO = 0, MYOS_DECODE_KERNELS = 1, MYOS_DECODE_PERSISTENT = 2,
+       MYOS_DECODE_STREAMED = 3 };
 int myos_set_decode_mode(myos_model *m, int mode);
 int myos_decode_path(const myos_model *m);
 /* Measurement hook for the persistent path (no reference counterpart): from

@@ -36,9 +36,17 @@ def to_block_shape(s, tied=True):
                            tied_head=tied)
 
 
-def open_persistent(path, s, kv, max_seq):
+# the two cooperative kernels: register-resident (PERSISTENT, the default
+# where it fits) and streamed (STREAMED, the default where only it fits)
+KERNELS = [pytest.param(myos.DECODE_PERSISTENT, id="register"),
+           pytest.param(myos.DECODE_STREAMED, id="streamed")]
+
+
+def open_persistent(path, s, kv, max_seq, mode=myos.DECODE_PERSISTENT):
     g = myos.Model.open(path, to_block_shape(s), kv, max_seq)
-    if g.decode_path() != myos.DECODE_PERSISTENT:
+    if mode == myos.DECODE_STREAMED:
+        g.set_decode_mode(myos.DECODE_STREAMED)
+    if g.decode_path() != mode:
         g.close()
         pytest.skip("the device cannot hold the cooperative decode grid")
     return g
@@ -57,14 +65,15 @@ SMALL = [(256, 4, 2, 64, 512, 1000, 3), (128, 6, 1, 32, 384, 777, 2),
          (384, 12, 2, 32, 1000, 4099, 2), (512, 4, 1, 128, 1536, 2048, 2)]
 
 
+@pytest.mark.parametrize("mode", KERNELS)
 @pytest.mark.parametrize("dims", SMALL)
-def test_persistent_small_models(tmp_path, dims):
+def test_persistent_small_models(tmp_path, dims, mode):
     s = shape_dict(*dims, 1e-6)
     t = random_map(s, seed=sum(dims) + 1, std=0.05)
     path = str(tmp_path / "m.safetensors")
     write_safetensors(path, t)
     max_seq = 80
-    g = open_persistent(path, s, myos.KV_F32, max_seq)
+    g = open_persistent(path, s, myos.KV_F32, max_seq, mode)
     k = myos.Model.open(path, to_block_shape(s), myos.KV_F32, max_seq)
     k.set_decode_mode(myos.DECODE_KERNELS)
     assert k.decode_path() == myos.DECODE_KERNELS
@@ -96,8 +105,9 @@ def test_persistent_small_models(tmp_path, dims):
     k.close()
 
 
+@pytest.mark.parametrize("mode", KERNELS)
 @pytest.mark.parametrize("dims", SMALL[:2] + SMALL[3:])
-def test_persistent_forced_small_models(tmp_path, dims):
+def test_persistent_forced_small_models(tmp_path, dims, mode):
     """decode_forced on the cooperative kernel: each step feeds the given id
     and reports the greedy id of the logits it started from; checked step by
     step against the oracle fed the same ids, and the per-kernel path."""
@@ -105,7 +115,7 @@ def test_persistent_forced_small_models(tmp_path, dims):
     t = random_map(s, seed=sum(dims) + 2, std=0.05)
     path = str(tmp_path / "m.safetensors")
     write_safetensors(path, t)
-    g = open_persistent(path, s, myos.KV_F32, 64)
+    g = open_persistent(path, s, myos.KV_F32, 64, mode)
     k = myos.Model.open(path, to_block_shape(s), myos.KV_F32, 64)
     k.set_decode_mode(myos.DECODE_KERNELS)
     o = oracle.Model(s, t, 64, threads=4)
@@ -137,8 +147,9 @@ def test_persistent_forced_small_models(tmp_path, dims):
     k.close()
 
 
+@pytest.mark.parametrize("mode", KERNELS)
 @pytest.mark.parametrize("dims", SMALL[:2] + SMALL[3:])
-def test_persistent_bf16_cache(tmp_path, dims):
+def test_persistent_bf16_cache(tmp_path, dims, mode):
     """A bf16 KV cache: the cooperative kernel stores and reads bf16 rows
     (rounded to nearest even, as the per-kernel path stores them). Against
     the f32-cache oracle, ids follow at BF16_GAP and logits within 2e-2; the
@@ -147,7 +158,7 @@ def test_persistent_bf16_cache(tmp_path, dims):
     t = random_map(s, seed=sum(dims) + 3, std=0.05)
     path = str(tmp_path / "m.safetensors")
     write_safetensors(path, t)
-    g = open_persistent(path, s, myos.KV_BF16, 80)
+    g = open_persistent(path, s, myos.KV_BF16, 80, mode)
     k = myos.Model.open(path, to_block_shape(s), myos.KV_BF16, 80)
     k.set_decode_mode(myos.DECODE_KERNELS)
     o = oracle.Model(s, t, 80, threads=4)
@@ -172,17 +183,19 @@ def test_persistent_bf16_cache(tmp_path, dims):
     k.close()
 
 
+@pytest.mark.parametrize("mode", KERNELS)
 @pytest.mark.parametrize("dims", [SMALL[0], SMALL[3]])
-def test_persistent_split_merge(tmp_path, dims):
-    """max_seq 600 gives 19 attention chunks per head: the cooperative kernel
-    then merges each head on four workgroups of head_dim / 4 columns. Prompt
-    of 530 ids, 40 greedy steps, the oracle following."""
+def test_persistent_split_merge(tmp_path, dims, mode):
+    """max_seq 600 gives 19 attention chunks per head: the register kernel
+    then merges each head on four workgroups of head_dim / 4 columns (the
+    streamed kernel merges a head on one workgroup). Prompt of 530 ids, 40
+    greedy steps, the oracle following."""
     s = shape_dict(*dims, 1e-6)
     t = random_map(s, seed=sum(dims) + 5, std=0.05)
     path = str(tmp_path / "m.safetensors")
     write_safetensors(path, t)
     max_seq = 600
-    g = open_persistent(path, s, myos.KV_F32, max_seq)
+    g = open_persistent(path, s, myos.KV_F32, max_seq, mode)
     o = oracle.Model(s, t, max_seq, threads=4)
     prompt = np.random.default_rng(13).integers(0, s["vocab"], 530)
     g.prefill(prompt)
@@ -195,12 +208,13 @@ def test_persistent_split_merge(tmp_path, dims):
     g.close()
 
 
-def test_persistent_until_cache_full(tmp_path):
+@pytest.mark.parametrize("mode", KERNELS)
+def test_persistent_until_cache_full(tmp_path, mode):
     s = shape_dict(256, 4, 2, 64, 512, 1000, 2, 1e-6)
     t = random_map(s, seed=5, std=0.05)
     path = str(tmp_path / "m.safetensors")
     write_safetensors(path, t)
-    g = open_persistent(path, s, myos.KV_F32, 12)
+    g = open_persistent(path, s, myos.KV_F32, 12, mode)
     o = oracle.Model(s, t, 12, threads=2)
     g.prefill([3, 1, 4])
     assert o.prefill([3, 1, 4]) == 0
@@ -212,7 +226,8 @@ def test_persistent_until_cache_full(tmp_path):
     assert_logits_parity(g.logits(), o.logits(), "at cache full")
 
 
-def test_persistent_wait_error_poisons_the_model(tmp_path):
+@pytest.mark.parametrize("mode", KERNELS)
+def test_persistent_wait_error_poisons_the_model(tmp_path, mode):
     """The error path of the bounded waits, forced from the host: with the
     kernel's error word raised before the launch, every wait gives up at once
     (the kernel still runs to its end), greedy_decode reports Hip and the
@@ -222,7 +237,7 @@ def test_persistent_wait_error_poisons_the_model(tmp_path):
     t = random_map(s, seed=7, std=0.05)
     path = str(tmp_path / "m.safetensors")
     write_safetensors(path, t)
-    g = open_persistent(path, s, myos.KV_F32, 40)
+    g = open_persistent(path, s, myos.KV_F32, 40, mode)
     prompt = [5, 9, 2, 7]
     g.prefill(prompt)
     g.debug_raise_wait_error()
@@ -294,4 +309,25 @@ def test_persistent_qwen15_s1_bf16_cache(qwen15):
     assert max_rel(g.logits(), o.logits()) < 2e-2
     assert max_rel(g.hidden(), o.hidden()) < 2e-2
     check_kv(g, o, s, (0, 127, 175), 2e-2, heads=[1])
+    g.close()
+
+
+def test_streamed_qwen15_s1_128_greedy(qwen15):
+    """The streamed cooperative kernel on the S1 workload (it fits the 1.5B
+    shape too): 128 greedy steps, every id under the tolerance rule with the
+    oracle following, then the final logits, hidden state and cache rows."""
+    path, s, t = qwen15
+    prompt = np.random.default_rng(2024).integers(0, 151936, 128)
+    g = open_persistent(path, s, myos.KV_F32, 256, myos.DECODE_STREAMED)
+    o = oracle.Model(s, t, 256, threads=16)
+    g.prefill(prompt)
+    assert o.prefill(prompt) == 0
+    ids_g = g.greedy_decode(128)
+    exact = follow_ids(o, ids_g, "S1 streamed")
+    print(f"S1 streamed: {exact}/128 ids equal the oracle's own argmax; decode "
+          f"{g.last_decode_ms():.2f} ms")
+    assert g.cache_len() == o.cache_len() == 256
+    assert_logits_parity(g.logits(), o.logits(), "after 128 streamed steps")
+    assert max_rel(g.hidden(), o.hidden()) < 1e-2
+    check_kv(g, o, s, (0, 127, 128, 255), 1e-2, heads=[0, 1])
     g.close()
