@@ -184,10 +184,14 @@ struct PersistArgs {
   uint64_t *trace;             // optional [grid][5 L + 3] phase timestamps of one step
   uint32_t trace_step;
   // streamed kernel: f32 activation buffers (wide_buffer_floats) and one
-  // barrier flag word per workgroup (zeroed once; tags only grow)
+  // barrier flag word per workgroup, kWFlagStride words apart (zeroed once;
+  // tags only grow)
   float *wide;
   uint64_t *wflags;
 };
+// words between two workgroups' barrier flags: one flag per 128-byte line, so
+// flags published at the same moment do not queue on a shared line
+constexpr int kWFlagStride = 16;
 int persist_grid();                       // workgroups per launch
 int persist_tags_per_step(int layers);
 size_t persist_part_words(int nq, int max_seq, int d);

@@ -442,7 +442,7 @@ int setup_persistent(myos_model *m) {
   if (!reg)
     for (size_t &w : words) w = 0;
   const size_t wide_f = wide ? wide_buffer_floats(a.H, a.I, a.nq, a.d, a.max_seq) : 0;
-  const size_t flags = wide ? (size_t)persist_grid() : 0;
+  const size_t flags = wide ? (size_t)persist_grid() * kWFlagStride : 0;
   size_t total = 0;
   for (size_t w : words) total += align256(w * 8);
   total += align256(wide_f * 4) + align256(flags * 8) + 256;

@@ -1273,12 +1273,12 @@ template <class Pf>
 __device__ __forceinline__ bool wide_barrier(const PersistArgs &a, uint32_t tag, int *fail, Pf pf) {
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
-  if (threadIdx.x == 0) tput(a.wflags + blockIdx.x, 0.f, tag);
+  if (threadIdx.x == 0) tput(a.wflags + blockIdx.x * kWFlagStride, 0.f, tag);
   pf();
   bool ok = *fail == 0;
   if (threadIdx.x < NB && ok) {
     for (unsigned spins = 0;; spins++) {
-      const uint64_t w = tload(a.wflags + threadIdx.x);
+      const uint64_t w = tload(a.wflags + threadIdx.x * kWFlagStride);
       if ((uint32_t)(w >> 32) >= tag) break;
       if (spin_fail(a, spins)) {
         ok = false;
