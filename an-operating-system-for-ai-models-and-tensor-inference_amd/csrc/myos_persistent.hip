@@ -1318,12 +1318,36 @@ __device__ __forceinline__ void wld(u32x4 (&t)[WRB][C], const uint16_t *W, int k
   for (int rb = 0; rb < WRB; rb++) ldrow_all<C>(t[rb], W, k, row + rb, last, lane);
 }
 
+// this lane's chunks of x (chunk lane + 64 i, 8 floats each) from LDS as
+// 16-byte reads (x is 16-byte aligned)
+template <int C>
+__device__ __forceinline__ void wload_x(float4 (&xr)[C][2], const float *x, int k, int lane) {
+  const int nch = k >> 3;
+  const float4 *x4 = (const float4 *)__builtin_assume_aligned(x, 16);
+  if (nch == 64 * C) {  // every lane holds C whole chunks: no guards
+#pragma unroll
+    for (int i = 0; i < C; i++) {
+      const int c = lane + i * 64;
+      xr[i][0] = x4[2 * c];
+      xr[i][1] = x4[2 * c + 1];
+    }
+    return;
+  }
+  const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+  for (int i = 0; i < C; i++) {
+    const int c = lane + i * 64;
+    xr[i][0] = c < nch ? x4[2 * c] : z;
+    xr[i][1] = c < nch ? x4[2 * c + 1] : z;
+  }
+}
+
 // RMSNorm of x (LDS, k floats) into this lane's chunks (lane + 64 i), f32;
 // the bf16 gains g in global memory or LDS
 template <int C>
 __device__ __forceinline__ void wnorm(float4 (&xr)[C][2], const float *x, const uint16_t *g, int k,
                                       float eps, int lane) {
-  load_x<C>(xr, x, k, lane);
+  wload_x<C>(xr, x, k, lane);
   float ss = 0.f;
 #pragma unroll
   for (int i = 0; i < C; i++) {
@@ -1332,10 +1356,11 @@ __device__ __forceinline__ void wnorm(float4 (&xr)[C][2], const float *x, const 
   }
   const float inv = 1.0f / sqrtf(wave_sum(ss) / (float)k + eps);
   const int nch = k >> 3;
+  const bool full = nch == 64 * C;
 #pragma unroll
   for (int i = 0; i < C; i++) {
     const int c = lane + i * 64;
-    if (c < nch) {
+    if (full || c < nch) {
       const u32x4 gw = *(const u32x4 *)(g + c * 8);
       xr[i][0] = make_float4(bf_lo(gw.x) * (xr[i][0].x * inv), bf_hi(gw.x) * (xr[i][0].y * inv),
                              bf_lo(gw.y) * (xr[i][0].z * inv), bf_hi(gw.y) * (xr[i][0].w * inv));
@@ -1886,7 +1911,7 @@ __global__ void __launch_bounds__(NT) decode_wide_kernel(PersistArgs a) {
         cload_vec(xs, B.att, qdim, tid);
         __syncthreads();
         float4 xr[C][2];
-        load_x<C>(xr, xs, qdim, lane);
+        wload_x<C>(xr, xs, qdim, lane);
         wstream<C>(pre, Ly.wo, qdim, o0r, o1r, xr, wave, lane, [&](int r, float y0, float y1) {
           if (lane != 0) return;
           cstore(B.xo + r, xol[r - o0r] + y0);
