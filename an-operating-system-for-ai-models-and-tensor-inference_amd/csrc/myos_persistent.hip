@@ -1343,9 +1343,9 @@ __device__ __forceinline__ void wload_x(float4 (&xr)[C][2], const float *x, int 
 }
 
 // RMSNorm of x (LDS, k floats) into this lane's chunks (lane + 64 i), f32;
-// the bf16 gains g in global memory or LDS
+// the bf16 gains g in global memory or LDS. Returns the 1 / rms factor
 template <int C>
-__device__ __forceinline__ void wnorm(float4 (&xr)[C][2], const float *x, const uint16_t *g, int k,
+__device__ __forceinline__ float wnorm(float4 (&xr)[C][2], const float *x, const uint16_t *g, int k,
                                       float eps, int lane) {
   wload_x<C>(xr, x, k, lane);
   float ss = 0.f;
@@ -1368,6 +1368,7 @@ __device__ __forceinline__ void wnorm(float4 (&xr)[C][2], const float *x, const 
                              bf_lo(gw.w) * (xr[i][1].z * inv), bf_hi(gw.w) * (xr[i][1].w * inv));
     }
   }
+  return inv;
 }
 
 // Rows [r0, r1) of W [rows, k]: wave w takes the row pairs r0 + 2 (w + NW j).
@@ -1518,6 +1519,7 @@ __global__ void __launch_bounds__(NT) decode_wide_kernel(PersistArgs a) {
   __shared__ float2 qcs_s[WQP / 2];  // RoPE (cos, sin) of its pairs at the step's position
   __shared__ int last_s;
   __shared__ int tile_s[2];
+  __shared__ float2 red2_s[NW];
 
   // tid and lane are re-derived at the top of every step and layer (see
   // opaque), so per-lane addresses are not hoisted out of the loops and held
@@ -1674,12 +1676,25 @@ __global__ void __launch_bounds__(NT) decode_wide_kernel(PersistArgs a) {
 
       // ---- QKV + bias + RoPE + KV store ----------------------------------------
       {
+        // one row pair past a pair per wave (18 rows at the 7B shape) is
+        // split by columns over the waves instead of a second round trip on
+        // wave 0: wave w takes chunks [w spc, (w + 1) spc), loaded before x;
+        // rows past the split read at byte offset 2^31 (zeros, no traffic)
+        const int qs1 = min(q1, q0 + 2 * NW), nsp = q1 - qs1;
+        const bool split = nsp > 0 && nsp <= 2;
+        const int nchh = H >> 3, spc = (nchh + NW - 1) / NW, sc = wave * spc + lane;
+        const bool sl = split && lane < spc && sc < nchh;
+        const __amdgpu_buffer_rsrc_t rsq = wrsrc(Ly.wqkv);
+        const u32x4 sw0 =
+            __builtin_amdgcn_raw_buffer_load_b128(rsq, sc * 16, sl ? qs1 * H * 2 : (int)0x80000000u, 2);
+        const u32x4 sw1 =
+            __builtin_amdgcn_raw_buffer_load_b128(rsq, sc * 16, sl ? (q1 - 1) * H * 2 : (int)0x80000000u, 2);
         if (l > 0) cload_vec(xs, B.x, H, tid);
         __syncthreads();
         if (tid < o1r - o0r) xol[tid] = xs[o0r + tid];
         float4 xr[C][2];
-        wnorm<C>(xr, xs, gn_s, H, a.eps, lane);
-        wstream<C>(pre, Ly.wqkv, H, q0, q1, xr, wave, lane, [&](int r, float y0, float y1) {
+        const float inv = wnorm<C>(xr, xs, gn_s, H, a.eps, lane);
+        auto qepi = [&](int r, float y0, float y1) {
           if (lane != 0) return;
           const float b0 = y0 + qb_s[r - q0], b1 = y1 + qb_s[r - q0 + 1];
           if (r < qdim + kvdim) {
@@ -1701,7 +1716,40 @@ __global__ void __launch_bounds__(NT) decode_wide_kernel(PersistArgs a) {
             kvstore<KB>(vc, base, b0);
             kvstore<KB>(vc, base + 1, b1);
           }
-        });
+        };
+        wstream<C>(pre, Ly.wqkv, H, q0, split ? qs1 : q1, xr, wave, lane, qepi);
+        if (split) {
+          float p0 = 0.f, p1 = 0.f;
+          if (sl) {
+            const float4 *x4 = (const float4 *)__builtin_assume_aligned(xs, 16);
+            const u32x4 gw = *(const u32x4 *)(gn_s + sc * 8);
+            const float4 a0 = x4[2 * sc], a1 = x4[2 * sc + 1];
+            const float xv[8] = {bf_lo(gw.x) * (a0.x * inv), bf_hi(gw.x) * (a0.y * inv),
+                                 bf_lo(gw.y) * (a0.z * inv), bf_hi(gw.y) * (a0.w * inv),
+                                 bf_lo(gw.z) * (a1.x * inv), bf_hi(gw.z) * (a1.y * inv),
+                                 bf_lo(gw.w) * (a1.z * inv), bf_hi(gw.w) * (a1.w * inv)};
+            const uint32_t w0[4] = {sw0.x, sw0.y, sw0.z, sw0.w}, w1[4] = {sw1.x, sw1.y, sw1.z, sw1.w};
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+              p0 = fmaf(bf_lo(w0[e]), xv[2 * e], p0);
+              p0 = fmaf(bf_hi(w0[e]), xv[2 * e + 1], p0);
+              p1 = fmaf(bf_lo(w1[e]), xv[2 * e], p1);
+              p1 = fmaf(bf_hi(w1[e]), xv[2 * e + 1], p1);
+            }
+          }
+          p0 = wave_sum(p0);
+          p1 = wave_sum(p1);
+          if (lane == 0) red2_s[wave] = make_float2(p0, p1);
+          __syncthreads();
+          if (tid == 0) {
+            float y0 = 0.f, y1 = 0.f;
+            for (int w = 0; w < NW; w++) {
+              y0 += red2_s[w].x;
+              y1 += red2_s[w].y;
+            }
+            qepi(qs1, y0, nsp > 1 ? y1 : 0.f);
+          }
+        }
       }
 
       // ---- attention partials for (kv head, chunk) items, merged by the last
