@@ -383,16 +383,16 @@ def main():
                          "GBps": round(by / (ms * 1e-3) / 1e9, 1)}
     log("per-kernel path: " + ", ".join(f"{n} {v['avg_us']}us {v['GBps']}GB/s"
                                         for n, v in kernels.items()))
-    tpath = os.path.join(ROOT, "profiles", "decode_traffic_qwen25_1_5b.json")
-    # the committed traffic figures are for the 1.5B shape with the f32 cache
-    tinfo = (json.load(open(tpath))
-             if os.path.exists(tpath) and kv == myos.KV_F32 and not is7b else {})
+    tpath = os.path.join(ROOT, "profiles",
+                         f"decode_traffic_qwen25_{'7b' if is7b else '1_5b'}.json")
+    # the committed traffic figures are for the f32 cache
+    tinfo = json.load(open(tpath)) if os.path.exists(tpath) and kv == myos.KV_F32 else {}
     if path_name in ("persistent", "streamed"):
         launch_bytes = b_tok * args.decode
         launch_s = dd / args.steps * 1e-3
         achieved = launch_bytes / launch_s
         traffic, tsrc = None, None
-        t = tinfo.get("persistent_launch") if path_name == "persistent" else None
+        t = tinfo.get(f"{path_name}_launch")
         if t and t.get("decode_steps") == args.decode and t.get("prompt_ids") == args.prompt:
             traffic, tsrc = t["traffic_bytes"], t["source"]
         roofline = {"bound": "hbm",
