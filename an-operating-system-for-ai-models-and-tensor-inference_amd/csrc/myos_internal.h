@@ -141,8 +141,14 @@ struct AttnPrefillArgs {
   const void *kc, *vc;
   int kv_bf16, max_seq, nq, nkv, head_dim, M, start_pos;
   uint16_t *out_hi, *out_lo;    // [M, nq*d]
+  float *part = nullptr;        // key-split partials (head_dim 128), part_cap floats
+  size_t part_cap = 0;
 };
 hipError_t launch_attn_prefill(const AttnPrefillArgs &a, hipStream_t s);
+// floats of the key-split partials for M queries of nq heads in ns splits
+inline size_t attn_prefill_part_floats(int nq, int M, int ns) {
+  return (size_t)nq * ns * M * (128 + 2);
+}
 
 hipError_t launch_permute_rows(uint16_t *dst, const uint16_t *src, const int *perm, int rows,
                                int cols, hipStream_t s);

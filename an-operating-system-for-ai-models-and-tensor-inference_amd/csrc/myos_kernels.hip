@@ -1742,7 +1742,11 @@ __global__ void __launch_bounds__(256) attn_prefill_mfma_kernel(AttnPrefillArgs 
   const int qpos = a.start_pos + (active ? qi : a.M - 1);
   const int last_pos = a.start_pos + min(a.M - 1, q0 + kFaQ - 1);  // the workgroup's last query
   const int wave_last = a.start_pos + min(a.M - 1, q0 + wave * 32 + 31);
-  const int nblk = last_pos / kFaK + 1;
+  // key split z of gridDim.z takes key blocks [b0, b1) of the query block's
+  // blocks [0, last_pos / kFaK]; with more than one split the workgroup writes
+  // f32 partials (o, max, sum) for attn_prefill_merge_kernel
+  const int ns = gridDim.z, nball = last_pos / kFaK + 1, bps = (nball + ns - 1) / ns;
+  const int b0 = min((int)blockIdx.z * bps, nball), nblk = min(b0 + bps, nball);
   // scores scaled by log2(e) / sqrt(d): the softmax runs on exp2
   const float scale2 = 1.4426950408889634f / sqrtf((float)kFaD);
   const int qd = a.nq * kFaD;
@@ -1851,14 +1855,14 @@ __global__ void __launch_bounds__(256) attn_prefill_mfma_kernel(AttnPrefillArgs 
     for (int e = 0; e < 16; e++) o[n][e] = 0.f;
   float mx = -INFINITY, l = 0.f;
 
-  gload(0);
+  gload(b0);
   sstore_k(0);
-  gload(1);
+  gload(b0 + 1);
   __syncthreads();
   sstore_vt(0);
   __syncthreads();
-  for (int b = 0; b < nblk; b++) {
-    const int st = b & 1;
+  for (int b = b0; b < nblk; b++) {
+    const int st = (b - b0) & 1;
     const int kb = b * kFaK;
     if (kb <= wave_last) {  // some query of the wave sees a key of the block
       const uint8_t *kh = fa_sm + st * kFaStage, *kl = kh + kFaK * kFaD * 2;
@@ -1953,7 +1957,7 @@ __global__ void __launch_bounds__(256) attn_prefill_mfma_kernel(AttnPrefillArgs 
   // last barrier), then each lane writes 8 consecutive dims of one query as
   // 16-byte hi / lo stores.
   float *orow = (float *)fa_sm + wave * 32 * (kFaD + 4);  // [32][d + 4] f32 per wave
-  const float inv = 1.0f / l;
+  const float inv = ns > 1 ? 1.0f : 1.0f / l;
 #pragma unroll
   for (int n = 0; n < 4; n++)
 #pragma unroll
@@ -1962,6 +1966,26 @@ __global__ void __launch_bounds__(256) attn_prefill_mfma_kernel(AttnPrefillArgs 
       orow[(lane & 31) * (kFaD + 4) + dim] = o[n][i] * inv;
     }
   __syncthreads();
+  if (ns > 1) {
+    // partial [h][z][query]: o (unnormalised, relative to the max) then (max, sum)
+    float *pbase = a.part + ((size_t)h * ns + blockIdx.z) * a.M * (kFaD + 2);
+    if (lane < 32 && active) {
+      pbase[(size_t)qi * (kFaD + 2) + kFaD] = mx;
+      pbase[(size_t)qi * (kFaD + 2) + kFaD + 1] = l;
+    }
+#pragma unroll
+    for (int r = 0; r < 8; r++) {
+      const int qq = r * 4 + (lane >> 4), c8 = (lane & 15) * 8;
+      const int qrow = q0 + wave * 32 + qq;
+      if (qrow < a.M) {
+        const float *src = orow + qq * (kFaD + 4) + c8;
+        float *dst = pbase + (size_t)qrow * (kFaD + 2) + c8;  // 8-byte aligned: d + 2 is even
+#pragma unroll
+        for (int e = 0; e < 8; e += 2) *(float2 *)(dst + e) = *(const float2 *)(src + e);
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int r = 0; r < 8; r++) {
     const int qq = r * 4 + (lane >> 4), c8 = (lane & 15) * 8;  // query of the wave, dims c8 .. + 7
@@ -1982,6 +2006,47 @@ __global__ void __launch_bounds__(256) attn_prefill_mfma_kernel(AttnPrefillArgs 
       *(bf16x8 *)(a.out_lo + idx) = lo;
     }
   }
+}
+
+// The key splits of attn_prefill_mfma_kernel merged in split order: thread t
+// takes 4 dims of one (query, head); out = sum_z 2^(m_z - M) o_z /
+// sum_z 2^(m_z - M) l_z with M = max_z m_z, as bf16 hi / lo planes.
+__global__ void __launch_bounds__(256) attn_prefill_merge_kernel(AttnPrefillArgs a, int ns) {
+  const size_t t = (size_t)blockIdx.x * 256 + threadIdx.x;
+  const size_t nvec = (size_t)a.M * a.nq * (kFaD / 4);
+  if (t >= nvec) return;
+  const int d4 = (int)(t % (kFaD / 4));
+  const size_t qh = t / (kFaD / 4);
+  const int h = (int)(qh % a.nq), q = (int)(qh / a.nq);
+  const size_t zs = (size_t)a.M * (kFaD + 2);  // one split's partials of a head
+  const float *p = a.part + (size_t)h * ns * zs + (size_t)q * (kFaD + 2);
+  float mmax = -INFINITY;
+  for (int z = 0; z < ns; z++) mmax = fmaxf(mmax, p[z * zs + kFaD]);
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  float lsum = 0.f;
+  for (int z = 0; z < ns; z++) {
+    const float *pz = p + z * zs;
+    const float m = pz[kFaD];
+    const float e = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - mmax);
+    lsum = fmaf(e, pz[kFaD + 1], lsum);
+    const float2 x0 = *(const float2 *)(pz + 4 * d4), x1 = *(const float2 *)(pz + 4 * d4 + 2);
+    acc.x = fmaf(e, x0.x, acc.x);
+    acc.y = fmaf(e, x0.y, acc.y);
+    acc.z = fmaf(e, x1.x, acc.z);
+    acc.w = fmaf(e, x1.y, acc.w);
+  }
+  const float inv = 1.0f / lsum;
+  const float v[4] = {acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv};
+  uint16_t hi[4], lo[4];
+#pragma unroll
+  for (int e = 0; e < 4; e++) {
+    const __bf16 hb = (__bf16)v[e];
+    hi[e] = __builtin_bit_cast(uint16_t, hb);
+    lo[e] = __builtin_bit_cast(uint16_t, (__bf16)(v[e] - (float)hb));
+  }
+  const size_t idx = (size_t)q * a.nq * kFaD + h * kFaD + 4 * d4;
+  *(uint2 *)(a.out_hi + idx) = make_uint2(hi[0] | ((uint32_t)hi[1] << 16), hi[2] | ((uint32_t)hi[3] << 16));
+  *(uint2 *)(a.out_lo + idx) = make_uint2(lo[0] | ((uint32_t)lo[1] << 16), lo[2] | ((uint32_t)lo[3] << 16));
 }
 
 inline unsigned nblk(size_t n, unsigned b) { return (unsigned)((n + b - 1) / b); }
@@ -2454,7 +2519,18 @@ hipError_t launch_attn_prefill(const AttnPrefillArgs &a, hipStream_t s) {
     }
     AttnPrefillArgs args = a;
     void *params[] = {&args};
-    return hipLaunchKernel(fn, dim3(a.nq, nblk((size_t)a.M, kFaQ)), dim3(256), params, kFaLds, s);
+    // fewer query-block workgroups than twice the CUs: split each block's keys
+    // four ways (when the workspace holds the partials)
+    const int nqb = (int)nblk((size_t)a.M, kFaQ);
+    const int nb_max = (a.start_pos + a.M - 1) / kFaK + 1;
+    int ns = a.nq * nqb < 512 ? std::min(4, nb_max) : 1;
+    if (ns > 1 && (!a.part || attn_prefill_part_floats(a.nq, a.M, ns) > a.part_cap)) ns = 1;
+    hipError_t e = hipLaunchKernel(fn, dim3(a.nq, nqb, ns), dim3(256), params, kFaLds, s);
+    if (e != hipSuccess || ns == 1) return e;
+    const size_t nvec = (size_t)a.M * a.nq * (kFaD / 4);
+    hipLaunchKernelGGL(attn_prefill_merge_kernel, dim3((unsigned)((nvec + 255) / 256)), dim3(256), 0, s,
+                       args, ns);
+    return hipGetLastError();
   }
   // 16-byte tile loads: the cache rows and q must be aligned to 4 elements
   if (a.head_dim == 128 || a.head_dim == 64 || a.head_dim == 32) {

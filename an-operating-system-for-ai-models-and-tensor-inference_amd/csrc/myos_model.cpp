@@ -372,6 +372,8 @@ int ensure_prefill(myos_model *m, size_t rows) {
   wsf = std::max(wsf, gemm_ws_floats(R, (int)H, (int)Q));
   wsf = std::max(wsf, gemm_ws_floats(R, (int)m->gu_rows, (int)H));
   wsf = std::max(wsf, gemm_ws_floats(R, (int)H, (int)I));
+  // the attention's key-split partials use the same space (between GEMMs)
+  if (m->s.head_dim == 128) wsf = std::max(wsf, attn_prefill_part_floats((int)m->s.num_q_heads, R, 4));
   const size_t bw = align256(wsf * 4);
   const size_t total = bx + bq + 2 * ba + 2 * bh + bt + bw;
   HIP_TRY(hipMalloc((void **)&m->pf, total));
@@ -941,6 +943,8 @@ int myos_prefill(myos_model *m, const uint32_t *tokens, size_t n) {
     ap.start_pos = (int)start;
     ap.out_hi = m->pAhi;  // the normed planes are dead after the QKV GEMM
     ap.out_lo = m->pAlo;
+    ap.part = m->pws;     // the QKV GEMM's partials are reduced by now
+    ap.part_cap = m->pws_cap;
     HIP_TRY(launch_attn_prefill(ap, st));
 
     GemmArgs o{};
