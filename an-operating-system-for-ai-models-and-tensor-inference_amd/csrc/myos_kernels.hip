@@ -2316,8 +2316,12 @@ using PfT32 = PfCfg<1, 1, 4, 1>;
 using PfT64 = PfCfg<1, 2, 4, 1>;
 using PfT128 = PfCfg<2, 2, 2, 2>;
 using PfT256 = PfCfg<2, 4, 2, 2>;
-constexpr int kPfCfgs = 4;
-constexpr int kPfBN[kPfCfgs] = {PfT32::BN, PfT64::BN, PfT128::BN, PfT256::BN};
+// 128 x 256 with eight waves (two per SIMD, 64 x 64 each): one wave's MFMAs
+// run while the other waits on LDS, which the four-wave 128 x 256 tile cannot
+using PfW256 = PfCfg<2, 2, 2, 4>;
+constexpr int kPfCfgs = 5;
+constexpr int kPfPlanCfgs = 4;  // the cost model's candidates (PfW256 is picked by shape)
+constexpr int kPfBN[kPfCfgs] = {PfT32::BN, PfT64::BN, PfT128::BN, PfT256::BN, PfW256::BN};
 constexpr int kCUs = 256;
 
 int g_force_cfg = -1, g_force_splits = 0;
@@ -2339,16 +2343,28 @@ GemmPlan pf_plan(int M, int N, int K) {
     best.splits = g_force_splits > 0 ? std::min(g_force_splits, K >> 6) : 1;
     return best;
   }
-  // Wide, short-K projections (gate/up: N >= 8192 rows of K <= 4096) run
-  // faster on the 128 x 64 single-stage kernel, whose 46 KB of LDS lets three
-  // workgroups share a CU: measured inside the 1.5B prefill, 128 ids 3.50 ->
-  // 3.28 ms and 2048 ids 24.8 -> 22.5 ms (the same swap for the down and
-  // the small projections measured no better or slower).
-  if (N >= 8192 && K <= 4096) return best;
+  // Wide, short-K projections (gate/up: N >= 8192 rows of K <= 4096), and
+  // long-K ones (down) over many rows, take the eight-wave 128 x 256 tile.
+  // Measured per launch with the split reduction, weights from HBM (1.5B
+  // shapes): gate/up at 128 rows 48.3 us on the single-stage 128 x 64 kernel
+  // -> 45.4 (three splits), at 2048 rows 380 -> 326; down at 2048 rows 175
+  // (128 x 256, four waves, two splits) -> 140. The small projections and
+  // down at 128 rows stay on the cost model's choice (the eight-wave tiles
+  // measured no better there).
+  if (N >= 8192 && K <= 4096) {
+    best.cfg = 4;
+    best.splits = M <= 256 ? std::min(3, K >> 6) : 1;
+    return best;
+  }
+  if (M > 256 && N <= 4096 && K >= 4096) {
+    best.cfg = 4;
+    best.splits = 2;
+    return best;
+  }
   const int nks = K >> 6;
   const long mt = (M + 127) / 128;
   double best_t = 1e30;
-  for (int c = 0; c < kPfCfgs; c++) {
+  for (int c = 0; c < kPfPlanCfgs; c++) {
     const long tiles = mt * ((N + kPfBN[c] - 1) / kPfBN[c]);
     const double stage = (32768.0 + 128.0 * kPfBN[c]) / 14.0;  // clocks per K stage
     for (int sp = 1; sp <= std::min(nks, 64); sp++) {
@@ -2432,6 +2448,7 @@ static hipError_t go_pf_cfg(const GemmArgs &a, int cfg, int splits, hipStream_t 
     case 1: return go_pf<PfT64, EPI>(a, splits, s);
     case 2: return go_pf<PfT128, EPI>(a, splits, s);
     case 3: return go_pf<PfT256, EPI>(a, splits, s);
+    case 4: return go_pf<PfW256, EPI>(a, splits, s);
     default: return hipErrorInvalidValue;
   }
 }
