@@ -316,6 +316,25 @@ __device__ __forceinline__ float seg_sum(float v, int S) {
   if (S >= 32) v += dpp<0x142, 0xA>(v, 0.f);
   return v;
 }
+// seg_sum over N values at once: each DPP step runs over all of them, so the
+// steps' latencies overlap
+template <int N>
+__device__ __forceinline__ void seg_sum_n(float (&v)[N], int S) {
+#pragma unroll
+  for (int i = 0; i < N; i++) v[i] += dpp<0xB1>(v[i], 0.f);
+#pragma unroll
+  for (int i = 0; i < N; i++) v[i] += dpp<0x4E>(v[i], 0.f);
+#pragma unroll
+  for (int i = 0; i < N; i++) v[i] += dpp<0x141>(v[i], 0.f);
+  if (S >= 16) {
+#pragma unroll
+    for (int i = 0; i < N; i++) v[i] += dpp<0x140>(v[i], 0.f);
+  }
+  if (S >= 32) {
+#pragma unroll
+    for (int i = 0; i < N; i++) v[i] += dpp<0x142, 0xA>(v[i], 0.f);
+  }
+}
 __device__ __forceinline__ bool seg_leader(int lane, int S) {
   return (lane & (S - 1)) == (S == 32 ? 16 : 0);
 }
@@ -1762,6 +1781,7 @@ __global__ void __launch_bounds__(NT) decode_wide_kernel(PersistArgs a) {
       // barrier; this step's row (written by the QKV phase) after it.
       const int nch = (seq + AC - 1) / AC;
       const int dq = d >> 2, j4 = tid & (dq - 1);
+      const int ld = __builtin_ctz(d), ldq = ld - 2;  // d is a power of two
       const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
           kc, (short)0, (int)(a.layer_kv * kvb), 0x00020000);
       const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
@@ -1772,7 +1792,7 @@ __global__ void __launch_bounds__(NT) decode_wide_kernel(PersistArgs a) {
         const int g = it % nkv, t0 = (it / nkv) * AC;
 #pragma unroll
         for (int u = 0; u < KV4; u++) {
-          const int t = (tid + u * NT) / dq;
+          const int t = (tid + u * NT) >> ldq;
           if (t >= tmin && t < tmax) {
             const uint32_t off = (uint32_t)((((size_t)g * a.max_seq + t0 + t) * d + j4 * 4) * kvb);
             if (KB) {
@@ -1828,12 +1848,12 @@ __global__ void __launch_bounds__(NT) decode_wide_kernel(PersistArgs a) {
 #pragma unroll
           for (int u = 0; u < 2; u++) {
             const int i = tid + u * NT;
-            if (i < gq * d) q_s[(i / d) * MAXD + (i % d)] = qv[u];
+            if (i < gq * d) q_s[(i >> ld) * MAXD + (i & (d - 1))] = qv[u];
           }
         }
 #pragma unroll
         for (int u = 0; u < KV4; u++) {
-          const int t = (tid + u * NT) / dq;
+          const int t = (tid + u * NT) >> ldq;
           if (t < n)
             *(float4 *)(v_s + t * MAXD + j4 * 4) =
                 make_float4(__uint_as_float(vr[u].x), __uint_as_float(vr[u].y),
@@ -1841,21 +1861,27 @@ __global__ void __launch_bounds__(NT) decode_wide_kernel(PersistArgs a) {
         }
         __syncthreads();
         const float scale = 1.0f / sqrtf((float)d);
+        // every head's partial dot first (rows past gq read stale LDS and are
+        // not stored), then the segmented sums over all heads at once
 #pragma unroll
         for (int u = 0; u < KV4; u++) {
-          const int t = (tid + u * NT) / dq;
+          const int t = (tid + u * NT) >> ldq;
           const float4 k4 = make_float4(__uint_as_float(kr[u].x), __uint_as_float(kr[u].y),
                                         __uint_as_float(kr[u].z), __uint_as_float(kr[u].w));
+          float sc[WMAXQ];
 #pragma unroll
           for (int h = 0; h < WMAXQ; h++) {
-            if (h >= gq) break;
             const float4 q4 = *(const float4 *)(q_s + h * MAXD + j4 * 4);
-            float sc = q4.x * k4.x;
-            sc = fmaf(q4.y, k4.y, sc);
-            sc = fmaf(q4.z, k4.z, sc);
-            sc = fmaf(q4.w, k4.w, sc);
-            sc = seg_sum(sc, dq);
-            if (t < n && seg_leader(lane, dq)) p_s[h * AC + t] = sc * scale;
+            float v = q4.x * k4.x;
+            v = fmaf(q4.y, k4.y, v);
+            v = fmaf(q4.z, k4.z, v);
+            sc[h] = fmaf(q4.w, k4.w, v);
+          }
+          seg_sum_n<WMAXQ>(sc, dq);
+          if (t < n && seg_leader(lane, dq)) {
+#pragma unroll
+            for (int h = 0; h < WMAXQ; h++)
+              if (h < gq) p_s[h * AC + t] = sc[h] * scale;
           }
         }
         __syncthreads();
@@ -1866,26 +1892,43 @@ __global__ void __launch_bounds__(NT) decode_wide_kernel(PersistArgs a) {
           const float e = lane < n ? expf(sc - mx) : 0.f;
           const float lsum = wave_sum(e);
           if (lane < AC) p_s[h * AC + lane] = e;
-          const int j0 = lane & (d - 1), j1 = (lane + 64) & (d - 1);
+          // lane l sums columns 2l and 2l + 1 (one 8-byte LDS read per position)
+          const int c2 = 2 * lane < d ? 2 * lane : 0;
           float o0 = 0.f, o1 = 0.f;
+          if (n == AC) {
 #pragma unroll
-          for (int t4 = 0; t4 < AC; t4 += 4) {
-            if (t4 < n) {
+            for (int t4 = 0; t4 < AC; t4 += 4) {
               const float4 e4 = *(const float4 *)(p_s + h * AC + t4);
               const float ev[4] = {e4.x, e4.y, e4.z, e4.w};
 #pragma unroll
               for (int k = 0; k < 4; k++) {
-                // rows past n hold stale LDS: masked, not just weighted by 0
-                const float *vt = v_s + (t4 + k) * MAXD;
-                const bool in = t4 + k < n;
-                o0 = fmaf(ev[k], in ? vt[j0] : 0.f, o0);
-                o1 = fmaf(ev[k], in ? vt[j1] : 0.f, o1);
+                const float2 v2 = *(const float2 *)(v_s + (t4 + k) * MAXD + c2);
+                o0 = fmaf(ev[k], v2.x, o0);
+                o1 = fmaf(ev[k], v2.y, o1);
+              }
+            }
+          } else {
+#pragma unroll
+            for (int t4 = 0; t4 < AC; t4 += 4) {
+              if (t4 < n) {
+                const float4 e4 = *(const float4 *)(p_s + h * AC + t4);
+                const float ev[4] = {e4.x, e4.y, e4.z, e4.w};
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                  // rows past n hold stale LDS: masked, not just weighted by 0
+                  const bool in = t4 + k < n;
+                  const float2 v2 = *(const float2 *)(v_s + (t4 + k) * MAXD + c2);
+                  o0 = fmaf(ev[k], in ? v2.x : 0.f, o0);
+                  o1 = fmaf(ev[k], in ? v2.y : 0.f, o1);
+                }
               }
             }
           }
           float *dst = B.part + ((size_t)(g * gq + h) * nchmax + c) * (d + 2);
-          if (lane < d) cstore(dst + lane, o0);
-          if (lane + 64 < d) cstore(dst + lane + 64, o1);
+          if (2 * lane < d) {
+            cstore(dst + 2 * lane, o0);
+            cstore(dst + 2 * lane + 1, o1);
+          }
           if (lane == 0) {
             cstore(dst + d, mx);
             cstore(dst + d + 1, lsum);
