@@ -853,20 +853,25 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
           float4 k4 = make_float4(__uint_as_float(kr[u].x), __uint_as_float(kr[u].y),
                                   __uint_as_float(kr[u].z), __uint_as_float(kr[u].w));
           if (t >= nold) k4 = t < n ? *(const float4 *)(kcur + j4 * 4) : make_float4(0.f, 0.f, 0.f, 0.f);
-          float4 q4s[8];
-#pragma unroll
-          for (int h = 0; h < 8; h++)
-            if (h < gq) q4s[h] = *(const float4 *)(q_s + h * d + j4 * 4);
+          // every head's partial dot, then the segmented sums over all heads
+          // at once (heads past gq are zeros and not stored)
+          float sc[8];
 #pragma unroll
           for (int h = 0; h < 8; h++) {
-            if (h >= gq) break;
-            const float4 q4 = q4s[h];
-            float sc = q4.x * k4.x;
-            sc = fmaf(q4.y, k4.y, sc);
-            sc = fmaf(q4.z, k4.z, sc);
-            sc = fmaf(q4.w, k4.w, sc);
-            sc = seg_sum(sc, dq);
-            if (t < n && seg_leader(lane, dq)) p_s[h * AC + t] = sc * scale;
+            sc[h] = 0.f;
+            if (h < gq) {
+              const float4 q4 = *(const float4 *)(q_s + h * d + j4 * 4);
+              float v = q4.x * k4.x;
+              v = fmaf(q4.y, k4.y, v);
+              v = fmaf(q4.z, k4.z, v);
+              sc[h] = fmaf(q4.w, k4.w, v);
+            }
+          }
+          seg_sum_n<8>(sc, dq);
+          if (t < n && seg_leader(lane, dq)) {
+#pragma unroll
+            for (int h = 0; h < 8; h++)
+              if (h < gq) p_s[h * AC + t] = sc[h] * scale;
           }
         }
         __syncthreads();
@@ -880,26 +885,43 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
           // broadcasts; lanes past the head's columns read in-row duplicates
           // and drop them
           if (lane < AC) p_s[h * AC + lane] = e;
-          const int j0 = lane & (d - 1), j1 = (lane + 64) & (d - 1);
+          // lane l sums columns 2l and 2l + 1 (one 8-byte LDS read per position)
+          const int c2 = 2 * lane < d ? 2 * lane : 0;
           float o0 = 0.f, o1 = 0.f;
+          if (n == AC) {
 #pragma unroll
-          for (int t4 = 0; t4 < AC; t4 += 4) {
-            if (t4 < n) {
+            for (int t4 = 0; t4 < AC; t4 += 4) {
               const float4 e4 = *(const float4 *)(p_s + h * AC + t4);
               const float ev[4] = {e4.x, e4.y, e4.z, e4.w};
 #pragma unroll
               for (int k = 0; k < 4; k++) {
-                // rows past n hold stale LDS: masked, not just weighted by 0
-                const float *vt = v_s + (t4 + k) * d;
-                const bool in = t4 + k < n;
-                o0 = fmaf(ev[k], in ? vt[j0] : 0.f, o0);
-                o1 = fmaf(ev[k], in ? vt[j1] : 0.f, o1);
+                const float2 v2 = *(const float2 *)(v_s + (t4 + k) * d + c2);
+                o0 = fmaf(ev[k], v2.x, o0);
+                o1 = fmaf(ev[k], v2.y, o1);
+              }
+            }
+          } else {
+#pragma unroll
+            for (int t4 = 0; t4 < AC; t4 += 4) {
+              if (t4 < n) {
+                const float4 e4 = *(const float4 *)(p_s + h * AC + t4);
+                const float ev[4] = {e4.x, e4.y, e4.z, e4.w};
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                  // rows past n hold stale LDS: masked, not just weighted by 0
+                  const bool in = t4 + k < n;
+                  const float2 v2 = *(const float2 *)(v_s + (t4 + k) * d + c2);
+                  o0 = fmaf(ev[k], in ? v2.x : 0.f, o0);
+                  o1 = fmaf(ev[k], in ? v2.y : 0.f, o1);
+                }
               }
             }
           }
           uint64_t *dst = a.tpart + ((size_t)(g * gq + h) * nchmax + c) * (d + 2);
-          if (lane < d) tput(dst + lane, o0, T + P_PART);
-          if (lane + 64 < d) tput(dst + lane + 64, o1, T + P_PART);
+          if (2 * lane < d) {
+            tput(dst + 2 * lane, o0, T + P_PART);
+            tput(dst + 2 * lane + 1, o1, T + P_PART);
+          }
           if (lane == 0) {
             tput(dst + d, mx, T + P_PART);
             tput(dst + d + 1, lsum, T + P_PART);
