@@ -452,10 +452,12 @@ def main():
                    "prompt_ids": args.prompt, "decode_steps": args.decode, "batch": 1,
                    "max_seq": max_seq, "kv_cache": args.kv,
                    "accumulate": "f32 accumulate over bf16 weights; activations enter the "
-                                 "products split into bf16 hi + lo terms (16 significant bits): "
-                                 "the MFMA prefill, and the cooperative decode kernel's "
-                                 "gate/up, down and head (v_dot2); its QKV, o and attention, "
-                                 "and the per-kernel decode path, keep f32 activations",
+                                 "products split into bf16 hi + lo terms (16 significant bits) "
+                                 "in the MFMA prefill" + (
+                                     " and in the register-resident decode kernel's gate/up, "
+                                     "down and head (v_dot2); its QKV, o and attention keep f32 "
+                                     "activations" if path_name == "persistent" else
+                                     "; the decode path keeps f32 activations"),
                    "decode_path": path_name, "graph": not args.no_graph,
                    "parallelism": "single GPU"},
         "prefill_tok_s": round(prefill_tok_s, 1),
