@@ -1218,19 +1218,21 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
 // call like decode_persistent_kernel, but every phase streams its weight rows
 // from HBM with the next row batch in flight, and phases meet at device-wide
 // barriers: a workgroup waits until its own stores have completed, publishes
-// a tagged flag word, and waits until all 256 flags carry the tag (or a later
-// one). Before each barrier every wave issues the loads of its first row
-// batch of the next phase (weights do not depend on the data), so the weight
-// stream keeps running across the wait. Activations cross workgroups through
-// f32 buffers with device-coherent (sc1) stores and loads. A layer is six
-// phases:
-//   QKV rows (+ bias, RoPE, KV-cache store) | attention items (kv head,
-//   32-position chunk) | merge per q head | o rows (+ residual) | RMSNorm +
-//   gate/up rows (+ SwiGLU) | down rows (+ residual)
+// a tagged flag word (one per 128-byte line), issues the loads of the next
+// phase's first row batch (weights do not depend on the data, so the weight
+// stream keeps running across the wait), and waits until all 256 flags carry
+// the tag or a later one. Activations cross workgroups through f32 buffers
+// with device-coherent (sc1) stores and loads. A layer is five phases:
+//   RMSNorm + QKV rows (+ bias, RoPE, KV-cache store) | attention items (kv
+//   head, 32-position chunk) on workgroups of their own, the last item of a
+//   kv group merging its heads | o rows (+ residual) | RMSNorm + gate/up rows
+//   (+ SwiGLU), in tiles handed out by ticket past a fixed share | down rows
+//   (+ residual)
 // then per step the final norm, the head rows with per-workgroup argmax
 // partials and the argmax, which every workgroup takes from the partials.
 // Numerics follow the per-kernel path: f32 FMAs over the bf16 weights in the
-// same row orders (qwen25_block.rs:220-304 per step).
+// same row orders (qwen25_block.rs:220-304 per step), except that a QKV row
+// pair past one pair per wave is summed by columns over the waves.
 constexpr int WDC = 5;    // 8-column chunks per thread of a down row: I <= 20480
 constexpr int WMR = 16;   // residual rows per workgroup: H <= 4096
 constexpr int WRB = 2;    // rows per wave batch
@@ -1242,8 +1244,8 @@ constexpr int WOR = 32;      // o rows per workgroup
 constexpr int WLMAX = 128;   // layers (the layer table sits in LDS)
 // barrier tags of a layer, in the order the phases run (a flag is compared
 // with >=, so they must grow)
-constexpr uint32_t W_QKV = 0, W_PART = 1, W_ATT = 2, W_XO = 3, W_H = 4, W_X = 5;
-static_assert(W_X < kTPL, "six barriers per layer");
+constexpr uint32_t W_QKV = 0, W_ATT = 1, W_XO = 2, W_H = 3, W_X = 4;
+static_assert(W_X < kTPL, "five barriers per layer");
 
 __host__ __device__ inline size_t wide_al(size_t n) { return (n + 63) & ~(size_t)63; }
 
