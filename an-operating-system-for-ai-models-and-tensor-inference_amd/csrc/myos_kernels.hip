@@ -1093,6 +1093,73 @@ __device__ __forceinline__ void gemm_store(const GemmArgs &a, int row, int col, 
   }
 }
 
+// The global reads of gemm_store for one element, issued ahead of the stores
+// of a batch (the stores may alias them to the compiler, so each element's
+// read would otherwise wait for the previous element's stores): EPI_RESID's
+// residual; EPI_QKV's bias pair and RoPE (cos, sin)
+struct EpiIn {
+  float2 u, v;
+};
+template <int EPI>
+__device__ __forceinline__ EpiIn gemm_epi_load(const GemmArgs &a, int row, int col) {
+  EpiIn in;
+  in.u = make_float2(0.f, 0.f);
+  in.v = make_float2(1.f, 0.f);
+  if (EPI == EPI_RESID) {
+    in.u.x = a.y[(size_t)row * a.N + col];
+  } else if (EPI == EPI_QKV) {
+    if ((col & 1) == 0) {
+      in.u = make_float2(a.bias[col], a.bias[col + 1]);
+      if (col < a.q_dim + a.kv_dim) {
+        const int half = a.head_dim >> 1;
+        const int rr = col < a.q_dim ? col : col - a.q_dim;
+        const int u = rr >> 1, p = u - (u / half) * half;
+        in.v = a.rope[(size_t)(a.start_pos + row) * half + p];
+      }
+    }
+  }
+  return in;
+}
+// gemm_store with the element's reads from gemm_epi_load
+template <int EPI>
+__device__ __forceinline__ void gemm_store_in(const GemmArgs &a, int row, int col, float c,
+                                              float partner, const EpiIn &in) {
+  if (EPI == EPI_RESID) {
+    a.y[(size_t)row * a.N + col] = in.u.x + c;
+  } else if (EPI == EPI_QKV) {
+    if ((col & 1) == 0) {
+      const int d = a.head_dim, half = d >> 1;
+      const int pos = a.start_pos + row;
+      const float y0 = c + in.u.x, y1 = partner + in.u.y;
+      if (col < a.q_dim + a.kv_dim) {
+        const bool is_q = col < a.q_dim;
+        const int rr = is_q ? col : col - a.q_dim;
+        const int u = rr >> 1, head = u / half, p = u - head * half;
+        const float2 cs = in.v;
+        const float o0 = y0 * cs.x - y1 * cs.y;
+        const float o1 = y1 * cs.x + y0 * cs.y;
+        if (is_q) {
+          float *qrow = a.q_out + (size_t)row * a.q_dim;
+          qrow[head * d + p] = o0;
+          qrow[head * d + p + half] = o1;
+        } else {
+          const size_t base = ((size_t)head * a.max_seq + pos) * d;
+          store_kv(a.kc, base + p, o0, a.kv_bf16);
+          store_kv(a.kc, base + p + half, o1, a.kv_bf16);
+        }
+      } else {
+        const int rr = col - a.q_dim - a.kv_dim;
+        const int head = rr / d, j = rr - head * d;
+        const size_t base = ((size_t)head * a.max_seq + pos) * d + j;
+        store_kv(a.vc, base, y0, a.kv_bf16);
+        store_kv(a.vc, base + 1, y1, a.kv_bf16);
+      }
+    }
+  } else {
+    gemm_store<EPI>(a, row, col, c, partner);
+  }
+}
+
 // One K tile of both operands: A (hi, lo) 128 rows x 8 octets, W 64 x 8;
 // thread tid holds octets tid + it * kBlock
 struct GemmTile {
@@ -1379,13 +1446,35 @@ __global__ void __launch_bounds__(C::NTH) gemm_pf_kernel(GemmArgs a) {
   __syncthreads();
   const bool split = S > 1;
   float *ws = a.ws + (size_t)z * M * N;
-  for (int idx = tid; idx < C::BM * C::BN; idx += C::NTH) {
-    const int tr = idx / C::BN, tc = idx % C::BN;
-    const int row = m0 + tr, col = n0 + tc;
-    if (row < M && col < N) {
-      const float c = cs[idx];
-      if (split) ws[(size_t)row * N + col] = c;
-      else gemm_store<EPI>(a, row, col, c, cs[idx ^ 1]);
+  if (split || EPI == EPI_STORE || EPI == EPI_GU) {
+    for (int idx = tid; idx < C::BM * C::BN; idx += C::NTH) {
+      const int tr = idx / C::BN, tc = idx % C::BN;
+      const int row = m0 + tr, col = n0 + tc;
+      if (row < M && col < N) {
+        const float c = cs[idx];
+        if (split) ws[(size_t)row * N + col] = c;
+        else gemm_store<EPI>(a, row, col, c, cs[idx ^ 1]);
+      }
+    }
+    return;
+  }
+  // the epilogues that read global memory: a batch of EB elements' reads
+  // first, then their stores
+  constexpr int NIT = C::BM * C::BN / C::NTH, EB = NIT % 8 == 0 ? 8 : 1;
+  static_assert(C::BM * C::BN % C::NTH == 0, "whole epilogue iterations");
+  for (int it0 = 0; it0 < NIT; it0 += EB) {
+    EpiIn in[EB];
+#pragma unroll
+    for (int e = 0; e < EB; e++) {
+      const int idx = tid + (it0 + e) * C::NTH;
+      const int row = m0 + idx / C::BN, col = n0 + idx % C::BN;
+      if (row < M && col < N) in[e] = gemm_epi_load<EPI>(a, row, col);
+    }
+#pragma unroll
+    for (int e = 0; e < EB; e++) {
+      const int idx = tid + (it0 + e) * C::NTH;
+      const int row = m0 + idx / C::BN, col = n0 + idx % C::BN;
+      if (row < M && col < N) gemm_store_in<EPI>(a, row, col, cs[idx], cs[idx ^ 1], in[e]);
     }
   }
 }
