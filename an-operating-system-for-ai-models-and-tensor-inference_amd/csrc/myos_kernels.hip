@@ -1816,11 +1816,6 @@ constexpr int kFaQ = 128, kFaK = 32, kFaD = 128;
 constexpr int kFaStage = 4 * kFaK * kFaD * 2;  // K hi, K lo, V^T hi, V^T lo (bf16)
 constexpr int kFaLds = 2 * kFaStage + kFaK * kFaD * 4;  // + the f32 V staging tile
 
-// V^T position of key kk (0..31) of a block
-__device__ __forceinline__ int fa_vpos(int kk) {
-  return (kk & 16) + (((kk >> 2) & 1) << 3) + (((kk >> 3) & 1) << 2) + (kk & 3);
-}
-
 __global__ void __launch_bounds__(256) attn_prefill_mfma_kernel(AttnPrefillArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t fa_sm[];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -1858,17 +1853,27 @@ __global__ void __launch_bounds__(256) attn_prefill_mfma_kernel(AttnPrefillArgs 
     }
   }
 
-  // block loader: thread t takes key t / 8 of the block, dims (t % 8) 16 .. + 15
+  // block loader: thread t takes key t / 8 of the block, dims (t % 8) 16 .. + 15.
+  // Buffer loads: a block past this split's range reads at byte offset 2^31,
+  // out of the descriptor's range (zeros, no traffic), so the pipeline's
+  // look-ahead loads cost nothing there and every load is still issued.
   const int lkey = tid >> 3, ldim = (tid & 7) * 16;
+  const uint32_t kvbytes = (uint32_t)((size_t)a.nkv * a.max_seq * kFaD * (a.kv_bf16 ? 2 : 4));
+  const __amdgpu_buffer_rsrc_t rkc =
+      __builtin_amdgcn_make_buffer_rsrc((void *)a.kc, (short)0, (int)kvbytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rvc =
+      __builtin_amdgcn_make_buffer_rsrc((void *)a.vc, (short)0, (int)kvbytes, 0x00020000);
   float kr[16], vr[16];
   auto gload = [&](int b) {
     const int kpos = min(b * kFaK + lkey, last_pos);
     const size_t base = ((size_t)g * a.max_seq + kpos) * kFaD + ldim;
+    const uint32_t esz = a.kv_bf16 ? 2u : 4u;
+    const int boff = b < nblk ? (int)(base * esz) : (int)0x80000000u;
     if (a.kv_bf16) {
 #pragma unroll
       for (int u = 0; u < 2; u++) {
-        const u32x4 kb = *(const u32x4 *)((const uint16_t *)a.kc + base + 8 * u);
-        const u32x4 vb = *(const u32x4 *)((const uint16_t *)a.vc + base + 8 * u);
+        const u32x4 kb = __builtin_amdgcn_raw_buffer_load_b128(rkc, boff, 16 * u, 0);
+        const u32x4 vb = __builtin_amdgcn_raw_buffer_load_b128(rvc, boff, 16 * u, 0);
         const uint32_t kw[4] = {kb.x, kb.y, kb.z, kb.w}, vw[4] = {vb.x, vb.y, vb.z, vb.w};
 #pragma unroll
         for (int e = 0; e < 4; e++) {
@@ -1881,10 +1886,12 @@ __global__ void __launch_bounds__(256) attn_prefill_mfma_kernel(AttnPrefillArgs 
     } else {
 #pragma unroll
       for (int u = 0; u < 4; u++) {
-        const float4 k4 = *(const float4 *)((const float *)a.kc + base + 4 * u);
-        const float4 v4 = *(const float4 *)((const float *)a.vc + base + 4 * u);
-        kr[4 * u] = k4.x; kr[4 * u + 1] = k4.y; kr[4 * u + 2] = k4.z; kr[4 * u + 3] = k4.w;
-        vr[4 * u] = v4.x; vr[4 * u + 1] = v4.y; vr[4 * u + 2] = v4.z; vr[4 * u + 3] = v4.w;
+        const u32x4 k4 = __builtin_amdgcn_raw_buffer_load_b128(rkc, boff, 16 * u, 0);
+        const u32x4 v4 = __builtin_amdgcn_raw_buffer_load_b128(rvc, boff, 16 * u, 0);
+        kr[4 * u] = __uint_as_float(k4.x); kr[4 * u + 1] = __uint_as_float(k4.y);
+        kr[4 * u + 2] = __uint_as_float(k4.z); kr[4 * u + 3] = __uint_as_float(k4.w);
+        vr[4 * u] = __uint_as_float(v4.x); vr[4 * u + 1] = __uint_as_float(v4.y);
+        vr[4 * u + 2] = __uint_as_float(v4.z); vr[4 * u + 3] = __uint_as_float(v4.w);
       }
     }
   };
@@ -2109,20 +2116,33 @@ __global__ void __launch_bounds__(256) attn_prefill_merge_kernel(AttnPrefillArgs
   const int h = (int)(qh % a.nq), q = (int)(qh / a.nq);
   const size_t zs = (size_t)a.M * (kFaD + 2);  // one split's partials of a head
   const float *p = a.part + (size_t)h * ns * zs + (size_t)q * (kFaD + 2);
+  // every split's (max, sum) and outputs in one round trip (ns <= 4)
+  float2 ml[4], x0[4], x1[4];
+#pragma unroll
+  for (int z = 0; z < 4; z++) {
+    if (z < ns) {
+      const float *pz = p + z * zs;
+      ml[z] = *(const float2 *)(pz + kFaD);
+      x0[z] = *(const float2 *)(pz + 4 * d4);
+      x1[z] = *(const float2 *)(pz + 4 * d4 + 2);
+    }
+  }
   float mmax = -INFINITY;
-  for (int z = 0; z < ns; z++) mmax = fmaxf(mmax, p[z * zs + kFaD]);
+#pragma unroll
+  for (int z = 0; z < 4; z++)
+    if (z < ns) mmax = fmaxf(mmax, ml[z].x);
   float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
   float lsum = 0.f;
-  for (int z = 0; z < ns; z++) {
-    const float *pz = p + z * zs;
-    const float m = pz[kFaD];
-    const float e = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - mmax);
-    lsum = fmaf(e, pz[kFaD + 1], lsum);
-    const float2 x0 = *(const float2 *)(pz + 4 * d4), x1 = *(const float2 *)(pz + 4 * d4 + 2);
-    acc.x = fmaf(e, x0.x, acc.x);
-    acc.y = fmaf(e, x0.y, acc.y);
-    acc.z = fmaf(e, x1.x, acc.z);
-    acc.w = fmaf(e, x1.y, acc.w);
+#pragma unroll
+  for (int z = 0; z < 4; z++) {
+    if (z < ns) {
+      const float e = ml[z].x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ml[z].x - mmax);
+      lsum = fmaf(e, ml[z].y, lsum);
+      acc.x = fmaf(e, x0[z].x, acc.x);
+      acc.y = fmaf(e, x0[z].y, acc.y);
+      acc.z = fmaf(e, x1[z].x, acc.z);
+      acc.w = fmaf(e, x1[z].y, acc.w);
+    }
   }
   const float inv = 1.0f / lsum;
   const float v[4] = {acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv};
@@ -2615,7 +2635,10 @@ hipError_t launch_gemm(const GemmArgs &args, GemvEpi epi, hipStream_t s) {
 
 hipError_t launch_attn_prefill(const AttnPrefillArgs &a, hipStream_t s) {
   if (a.head_dim > kMaxHeadDim) return hipErrorInvalidValue;
-  if (a.head_dim == kFaD && a.nq % a.nkv == 0) {
+  // the MFMA kernel's buffer loads address the layer's cache with 32-bit
+  // offsets and use 2^31 as the out-of-range offset
+  const size_t kv_bytes = (size_t)a.nkv * a.max_seq * a.head_dim * (a.kv_bf16 ? 2 : 4);
+  if (a.head_dim == kFaD && a.nq % a.nkv == 0 && kv_bytes < (size_t(1) << 31)) {
     static bool attr_done = false;
     const void *fn = (const void *)attn_prefill_mfma_kernel;
     if (!attr_done) {

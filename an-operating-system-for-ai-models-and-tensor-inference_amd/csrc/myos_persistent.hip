@@ -305,19 +305,10 @@ __device__ __forceinline__ float dotrow(const u32x4 (&t)[C], const float *x, int
   return wave_sum(s);
 }
 
-// Sum over aligned groups of S lanes, S = 8, 16 or 32 (wave-uniform). For
-// S <= 16 every lane of a group holds its total; for S = 32 lanes 16-31 and
-// 48-63 do.
-__device__ __forceinline__ float seg_sum(float v, int S) {
-  v += dpp<0xB1>(v, 0.f);
-  v += dpp<0x4E>(v, 0.f);
-  v += dpp<0x141>(v, 0.f);
-  if (S >= 16) v += dpp<0x140>(v, 0.f);
-  if (S >= 32) v += dpp<0x142, 0xA>(v, 0.f);
-  return v;
-}
-// seg_sum over N values at once: each DPP step runs over all of them, so the
-// steps' latencies overlap
+// Sum over aligned groups of S lanes, S = 8, 16 or 32 (wave-uniform), for N
+// values at once: each DPP step runs over all of them, so the steps'
+// latencies overlap. For S <= 16 every lane of a group holds its total; for
+// S = 32 lanes 16-31 and 48-63 do.
 template <int N>
 __device__ __forceinline__ void seg_sum_n(float (&v)[N], int S) {
 #pragma unroll
