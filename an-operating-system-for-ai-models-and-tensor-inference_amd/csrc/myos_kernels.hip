@@ -1333,15 +1333,19 @@ __global__ void __launch_bounds__(C::NTH) gemm_pf_kernel(GemmArgs a) {
       }
     }
   };
-  auto swrite = [&](int set, int st) {
+  // the register set's chunks into LDS stage `st`: the thread's stores are
+  // numbered e = 0 .. NW - 1 (A hi, A lo, W) and part p of np takes those with
+  // e * np / NW == p
+  constexpr int NW = 2 * C::ALD + C::WLD;
+  auto swrite = [&](int set, int st, int p, int np) {
     uint8_t *base = pf_sm + st * C::STAGE;
 #pragma unroll
     for (int i = 0; i < C::ALD; i++) {
       const int q = tid + i * C::NTH;
       if (C::ACH % C::NTH == 0 || q < C::ACH) {
         const int r = q >> 3, slot = ((q & 7) ^ (r & 7) ^ ((r >> 3) & 1)) << 4;
-        *(u32x4 *)(base + r * 128 + slot) = ra[set][i];
-        *(u32x4 *)(base + C::AL_OFF + r * 128 + slot) = rl[set][i];
+        if ((2 * i) * np / NW == p) *(u32x4 *)(base + r * 128 + slot) = ra[set][i];
+        if ((2 * i + 1) * np / NW == p) *(u32x4 *)(base + C::AL_OFF + r * 128 + slot) = rl[set][i];
       }
     }
 #pragma unroll
@@ -1349,7 +1353,7 @@ __global__ void __launch_bounds__(C::NTH) gemm_pf_kernel(GemmArgs a) {
       const int q = tid + i * C::NTH;
       if (C::WCH % C::NTH == 0 || q < C::WCH) {
         const int r = q >> 3, slot = ((q & 7) ^ (r & 7) ^ ((r >> 3) & 1)) << 4;
-        *(u32x4 *)(base + C::W_OFF + r * 128 + slot) = rb[set][i];
+        if ((2 * C::ALD + i) * np / NW == p) *(u32x4 *)(base + C::W_OFF + r * 128 + slot) = rb[set][i];
       }
     }
   };
@@ -1365,8 +1369,12 @@ __global__ void __launch_bounds__(C::NTH) gemm_pf_kernel(GemmArgs a) {
   const int arow = (wm * C::MB * 32 + (lane & 31)) * 128;
   const int wrow = (wn * C::NB * 32 + (lane & 31)) * 128;
   // the 64-wide stage in LDS stage `st`: 4 K steps of 16, each step's
-  // fragments read while the previous step's MFMAs run
-  auto mult = [&](int st) {
+  // fragments read while the previous step's MFMAs run. After each step's
+  // MFMAs a quarter of register set `wset` goes to the other LDS stage (last
+  // read before the previous barrier), so the next stage's stores share the
+  // LDS with this stage's reads instead of stalling every wave after the
+  // barrier.
+  auto mult = [&](int st, int wset) {
     const uint8_t *base = pf_sm + st * C::STAGE;
     bf16x8 fh[2][C::MB], fl[2][C::MB], fw[2][C::NB];
     auto ldfrag = [&](int buf, int ks) {
@@ -1385,6 +1393,9 @@ __global__ void __launch_bounds__(C::NTH) gemm_pf_kernel(GemmArgs a) {
     for (int ks = 0; ks < 4; ks++) {
       const int b = ks & 1;
       if (ks + 1 < 4) ldfrag(b ^ 1, ks + 1);
+      // scheduling fences: the next step's reads stay ahead of this step's
+      // MFMAs (the scheduler otherwise moves each read next to its use)
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int i = 0; i < C::MB; i++)
 #pragma unroll
@@ -1395,13 +1406,15 @@ __global__ void __launch_bounds__(C::NTH) gemm_pf_kernel(GemmArgs a) {
 #pragma unroll
         for (int j = 0; j < C::NB; j++)
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fl[b][i], fw[b][j], acc[i][j], 0, 0, 0);
+      swrite(wset, st ^ 1, ks, 4);
+      __builtin_amdgcn_sched_barrier(0);
     }
   };
 
   // stage s lives in register set s % R and LDS stage s & 1
   if (nst > 0) {
     gload(0, ks0);
-    swrite(0, 0);
+    swrite(0, 0, 0, 1);
 #pragma unroll
     for (int s = 1; s < R; s++) gload(s, ks0 + s);
   }
@@ -1411,9 +1424,8 @@ __global__ void __launch_bounds__(C::NTH) gemm_pf_kernel(GemmArgs a) {
 #pragma unroll
     for (int u = 0; u < R; u++) {
       const int it = it0 + u;
-      swrite((u + 1) % R, (it & 1) ^ 1);
       gload(u, ks0 + it + R);
-      mult(it & 1);
+      mult(it & 1, (u + 1) % R);
       __syncthreads();
     }
   }
@@ -1421,8 +1433,7 @@ __global__ void __launch_bounds__(C::NTH) gemm_pf_kernel(GemmArgs a) {
   for (int u = 0; u < R; u++) {
     const int it = nfull + u;
     if (it < nst) {
-      swrite((u + 1) % R, (it & 1) ^ 1);
-      mult(it & 1);
+      mult(it & 1, (u + 1) % R);
       __syncthreads();
     }
   }
