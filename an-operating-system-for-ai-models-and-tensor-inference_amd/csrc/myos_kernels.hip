@@ -1830,8 +1830,16 @@ constexpr int kFaLds = 2 * kFaStage + kFaK * kFaD * 4;  // + the f32 V staging t
 __global__ void __launch_bounds__(256) attn_prefill_mfma_kernel(AttnPrefillArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t fa_sm[];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int h = blockIdx.x, g = h / (a.nq / a.nkv);
-  const int q0 = blockIdx.y * kFaQ;
+  // Workgroups start in linear grid order (x fastest). A query block's work
+  // grows with its index under the causal mask, so linear id w takes query
+  // block nqb - 1 - w / (heads * splits) and, within it, head w % heads and
+  // key split (w / heads) % splits: the longest workgroups start first and
+  // the short ones fill the tail.
+  const int nh = gridDim.x, nqb = gridDim.y, ns = gridDim.z;
+  const int w = blockIdx.x + nh * (blockIdx.y + nqb * blockIdx.z);
+  const int rem = w % (nh * ns), h = rem % nh, zs = rem / nh;
+  const int g = h / (a.nq / a.nkv);
+  const int q0 = (nqb - 1 - w / (nh * ns)) * kFaQ;
   const int qi = q0 + wave * 32 + (lane & 31);  // this lane's query
   const bool active = qi < a.M;
   const int qpos = a.start_pos + (active ? qi : a.M - 1);
@@ -1840,8 +1848,8 @@ __global__ void __launch_bounds__(256) attn_prefill_mfma_kernel(AttnPrefillArgs 
   // key split z of gridDim.z takes key blocks [b0, b1) of the query block's
   // blocks [0, last_pos / kFaK]; with more than one split the workgroup writes
   // f32 partials (o, max, sum) for attn_prefill_merge_kernel
-  const int ns = gridDim.z, nball = last_pos / kFaK + 1, bps = (nball + ns - 1) / ns;
-  const int b0 = min((int)blockIdx.z * bps, nball), nblk = min(b0 + bps, nball);
+  const int nball = last_pos / kFaK + 1, bps = (nball + ns - 1) / ns;
+  const int b0 = min(zs * bps, nball), nblk = min(b0 + bps, nball);
   // scores scaled by log2(e) / sqrt(d): the softmax runs on exp2
   const float scale2 = 1.4426950408889634f / sqrtf((float)kFaD);
   const int qd = a.nq * kFaD;
@@ -2075,7 +2083,7 @@ __global__ void __launch_bounds__(256) attn_prefill_mfma_kernel(AttnPrefillArgs 
   __syncthreads();
   if (ns > 1) {
     // partial [h][z][query]: o (unnormalised, relative to the max) then (max, sum)
-    float *pbase = a.part + ((size_t)h * ns + blockIdx.z) * a.M * (kFaD + 2);
+    float *pbase = a.part + ((size_t)h * ns + zs) * a.M * (kFaD + 2);
     if (lane < 32 && active) {
       pbase[(size_t)qi * (kFaD + 2) + kFaD] = mx;
       pbase[(size_t)qi * (kFaD + 2) + kFaD + 1] = l;
