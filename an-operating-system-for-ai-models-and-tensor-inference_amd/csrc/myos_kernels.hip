@@ -1827,7 +1827,11 @@ constexpr int kFaQ = 128, kFaK = 32, kFaD = 128;
 constexpr int kFaStage = 4 * kFaK * kFaD * 2;  // K hi, K lo, V^T hi, V^T lo (bf16)
 constexpr int kFaLds = 2 * kFaStage + kFaK * kFaD * 4;  // + the f32 V staging tile
 
-__global__ void __launch_bounds__(256) attn_prefill_mfma_kernel(AttnPrefillArgs a) {
+// Two workgroups per CU (80 KB of LDS each): the bound caps the kernel at 256
+// registers a lane (248 VGPRs, no spills), where it otherwise took 340 and fit
+// one wave per SIMD; one workgroup's MFMAs then overlap the other's staging
+// and barriers.
+__global__ void __launch_bounds__(256, 2) attn_prefill_mfma_kernel(AttnPrefillArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t fa_sm[];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   // Workgroups start in linear grid order (x fastest). A query block's work
