@@ -1000,6 +1000,50 @@ __device__ __forceinline__ void split2(float x, uint16_t *hi, uint16_t *lo) {
   *lo = f2bf(x - bf16f(h));
 }
 
+// four consecutive normalised values g[e] * (x[e] * inv), as split2 writes
+// them, stored as one 8-byte word per plane (hi, lo 8-byte aligned)
+__device__ __forceinline__ void split4_store(float4 x, uint2 g, float inv, uint16_t *hi, uint16_t *lo) {
+  const float y[4] = {bf16f((uint16_t)(g.x & 0xffffu)) * (x.x * inv), bf16f((uint16_t)(g.x >> 16)) * (x.y * inv),
+                      bf16f((uint16_t)(g.y & 0xffffu)) * (x.z * inv), bf16f((uint16_t)(g.y >> 16)) * (x.w * inv)};
+  uint32_t h[4], l[4];
+#pragma unroll
+  for (int e = 0; e < 4; e++) {
+    const uint16_t hb = f2bf(y[e]);
+    h[e] = hb;
+    l[e] = f2bf(y[e] - bf16f(hb));
+  }
+  *(uint2 *)hi = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
+  *(uint2 *)lo = make_uint2(l[0] | (l[1] << 16), l[2] | (l[3] << 16));
+}
+
+// rmsnorm_rows_split_kernel for H % 4 == 0 and H <= 4 NV kBlock: the row's
+// values and gains are loaded once, up front, as float4 / 8-byte words
+template <int NV>
+__global__ void __launch_bounds__(kBlock)
+    rmsnorm_rows_split4_kernel(const float *X, const uint16_t *g, float eps, int H, uint16_t *hi,
+                               uint16_t *lo) {
+  __shared__ float red4[4];
+  const size_t r = blockIdx.x;
+  const int n4 = H >> 2;
+  float4 xv[NV];
+  uint2 gv[NV];
+  float ss = 0.f;
+#pragma unroll
+  for (int v = 0; v < NV; v++) {
+    const int c4 = threadIdx.x + v * kBlock;
+    xv[v] = c4 < n4 ? *(const float4 *)(X + r * H + 4 * c4) : make_float4(0.f, 0.f, 0.f, 0.f);
+    gv[v] = c4 < n4 ? *(const uint2 *)(g + 4 * c4) : make_uint2(0u, 0u);
+    ss += xv[v].x * xv[v].x + xv[v].y * xv[v].y + xv[v].z * xv[v].z + xv[v].w * xv[v].w;
+  }
+  const float tot = block_sum(ss, red4);
+  const float inv = 1.0f / sqrtf(tot / (float)H + eps);
+#pragma unroll
+  for (int v = 0; v < NV; v++) {
+    const int c4 = threadIdx.x + v * kBlock;
+    if (c4 < n4) split4_store(xv[v], gv[v], inv, hi + r * H + 4 * c4, lo + r * H + 4 * c4);
+  }
+}
+
 __global__ void __launch_bounds__(kBlock)
     rmsnorm_rows_split_kernel(const float *X, const uint16_t *g, float eps, int H, uint16_t *hi,
                               uint16_t *lo) {
@@ -1503,30 +1547,55 @@ __global__ void __launch_bounds__(kBlock) gemm_resid_norm_kernel(GemmArgs a, int
   const size_t MN = (size_t)a.M * H;
   const float *ws = a.ws + (size_t)r * H;
   float *y = a.y + (size_t)r * H;
-  float4 xv[NV];
+  // the residual and a batch of up to 8 splits for all NV column groups are
+  // loaded before any is added (one memory round trip per batch); each
+  // group's splits are added in split order
+  constexpr int ZB = 8;
+  float4 xv[NV], c[NV];
+  uint2 gv[NV];  // the group's four gains, loaded before any store
+#pragma unroll
+  for (int v = 0; v < NV; v++) {
+    const int c4 = threadIdx.x + v * kBlock;
+    c[v] = make_float4(0.f, 0.f, 0.f, 0.f);
+    xv[v] = c4 < n4 ? *(const float4 *)(y + 4 * c4) : make_float4(0.f, 0.f, 0.f, 0.f);
+    gv[v] = c4 < n4 ? *(const uint2 *)(g + 4 * c4) : make_uint2(0u, 0u);
+  }
+  for (int z0 = 0; z0 < splits; z0 += ZB) {
+    float4 w[ZB][NV];
+#pragma unroll
+    for (int dz = 0; dz < ZB; dz++)
+#pragma unroll
+      for (int v = 0; v < NV; v++) {
+        const int c4 = threadIdx.x + v * kBlock;
+        w[dz][v] = z0 + dz < splits && c4 < n4 ? *(const float4 *)(ws + (z0 + dz) * MN + 4 * c4)
+                                               : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+#pragma unroll
+    for (int dz = 0; dz < ZB; dz++)
+#pragma unroll
+      for (int v = 0; v < NV; v++)
+        if (z0 + dz < splits) {
+          c[v].x += w[dz][v].x;
+          c[v].y += w[dz][v].y;
+          c[v].z += w[dz][v].z;
+          c[v].w += w[dz][v].w;
+        }
+  }
   float ss = 0.f;
 #pragma unroll
   for (int v = 0; v < NV; v++) {
     const int c4 = threadIdx.x + v * kBlock;
-    xv[v] = make_float4(0.f, 0.f, 0.f, 0.f);
     if (c4 < n4) {
-      float4 c = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll 4
-      for (int z = 0; z < splits; z++) {
-        const float4 w = *(const float4 *)(ws + z * MN + 4 * c4);
-        c.x += w.x;
-        c.y += w.y;
-        c.z += w.z;
-        c.w += w.w;
-      }
-      float4 x = *(const float4 *)(y + 4 * c4);
-      x.x += c.x;
-      x.y += c.y;
-      x.z += c.z;
-      x.w += c.w;
+      float4 x = xv[v];
+      x.x += c[v].x;
+      x.y += c[v].y;
+      x.z += c[v].z;
+      x.w += c[v].w;
       *(float4 *)(y + 4 * c4) = x;
       xv[v] = x;
       ss += x.x * x.x + x.y * x.y + x.z * x.z + x.w * x.w;
+    } else {
+      xv[v] = make_float4(0.f, 0.f, 0.f, 0.f);
     }
   }
   const float tot = block_sum(ss, red4);
@@ -1534,12 +1603,7 @@ __global__ void __launch_bounds__(kBlock) gemm_resid_norm_kernel(GemmArgs a, int
 #pragma unroll
   for (int v = 0; v < NV; v++) {
     const int c4 = threadIdx.x + v * kBlock;
-    if (c4 < n4) {
-      const size_t o = (size_t)r * H + 4 * c4;
-      const float xe[4] = {xv[v].x, xv[v].y, xv[v].z, xv[v].w};
-#pragma unroll
-      for (int e = 0; e < 4; e++) split2(bf16f(g[4 * c4 + e]) * (xe[e] * inv), hi + o + e, lo + o + e);
-    }
+    if (c4 < n4) split4_store(xv[v], gv[v], inv, hi + (size_t)r * H + 4 * c4, lo + (size_t)r * H + 4 * c4);
   }
 }
 
@@ -1551,14 +1615,23 @@ __global__ void __launch_bounds__(kBlock) gemm_reduce4_kernel(GemmArgs a, int sp
   if (i >= (size_t)a.M * n4) return;
   const int row = (int)(i / (size_t)n4), col = 4 * (int)(i % (size_t)n4);
   const size_t MN = (size_t)a.M * a.N, off = (size_t)row * a.N + col;
+  // a batch of up to 8 splits is loaded before any is added (one memory round
+  // trip per batch); the splits are added in split order
+  constexpr int ZB = 8;
   float4 c = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll 4
-  for (int z = 0; z < splits; z++) {
-    const float4 w = *(const float4 *)(a.ws + z * MN + off);
-    c.x += w.x;
-    c.y += w.y;
-    c.z += w.z;
-    c.w += w.w;
+  for (int z0 = 0; z0 < splits; z0 += ZB) {
+    float4 w[ZB];
+#pragma unroll
+    for (int dz = 0; dz < ZB; dz++)
+      w[dz] = z0 + dz < splits ? *(const float4 *)(a.ws + (z0 + dz) * MN + off) : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int dz = 0; dz < ZB; dz++)
+      if (z0 + dz < splits) {
+        c.x += w[dz].x;
+        c.y += w[dz].y;
+        c.z += w[dz].z;
+        c.w += w[dz].w;
+      }
   }
   gemm_store<EPI>(a, row, col, c.x, c.y);
   gemm_store<EPI>(a, row, col + 1, c.y, c.x);
@@ -2427,8 +2500,17 @@ hipError_t launch_embed_rows(float *X, const uint16_t *embed, const uint32_t *to
 
 hipError_t launch_rmsnorm_rows_split(const float *X, const uint16_t *g, float eps, int M, int H,
                                      uint16_t *hi, uint16_t *lo, hipStream_t s) {
-  hipLaunchKernelGGL(rmsnorm_rows_split_kernel, dim3(M), dim3(kBlock), 0, s, X, g, eps, H, hi,
-                     lo);
+  const int n4 = H >> 2;
+  const bool vec = (H & 3) == 0 && n4 <= 4 * kBlock && ((uintptr_t)X & 15) == 0 &&
+                   (((uintptr_t)g | (uintptr_t)hi | (uintptr_t)lo) & 7) == 0;
+  if (!vec)
+    hipLaunchKernelGGL(rmsnorm_rows_split_kernel, dim3(M), dim3(kBlock), 0, s, X, g, eps, H, hi, lo);
+  else if (n4 <= kBlock)
+    hipLaunchKernelGGL(rmsnorm_rows_split4_kernel<1>, dim3(M), dim3(kBlock), 0, s, X, g, eps, H, hi, lo);
+  else if (n4 <= 2 * kBlock)
+    hipLaunchKernelGGL(rmsnorm_rows_split4_kernel<2>, dim3(M), dim3(kBlock), 0, s, X, g, eps, H, hi, lo);
+  else
+    hipLaunchKernelGGL(rmsnorm_rows_split4_kernel<4>, dim3(M), dim3(kBlock), 0, s, X, g, eps, H, hi, lo);
   return hipGetLastError();
 }
 
@@ -2608,7 +2690,8 @@ hipError_t launch_gemm_resid_norm(const GemmArgs &args, const uint16_t *g, float
   GemmArgs a = args;
   const int n4 = a.N >> 2;
   const bool can_fuse = (a.N & 3) == 0 && n4 <= 4 * kBlock &&
-                        (((uintptr_t)a.ws | (uintptr_t)a.y) & 15) == 0;
+                        (((uintptr_t)a.ws | (uintptr_t)a.y) & 15) == 0 &&
+                        (((uintptr_t)g | (uintptr_t)hi | (uintptr_t)lo) & 7) == 0;
   int splits = 1;
   hipError_t e = gemm_main<EPI_RESID>(a, s, &splits);
   if (e != hipSuccess) return e;
