@@ -1633,10 +1633,21 @@ __global__ void __launch_bounds__(kBlock) gemm_reduce4_kernel(GemmArgs a, int sp
         c.w += w[dz].w;
       }
   }
-  gemm_store<EPI>(a, row, col, c.x, c.y);
-  gemm_store<EPI>(a, row, col + 1, c.y, c.x);
-  gemm_store<EPI>(a, row, col + 2, c.z, c.w);
-  gemm_store<EPI>(a, row, col + 3, c.w, c.z);
+  if constexpr (EPI == EPI_RESID || EPI == EPI_QKV) {
+    // the epilogue's global reads for all four columns ahead of their stores
+    EpiIn in[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) in[e] = gemm_epi_load<EPI>(a, row, col + e);
+    gemm_store_in<EPI>(a, row, col, c.x, c.y, in[0]);
+    gemm_store_in<EPI>(a, row, col + 1, c.y, c.x, in[1]);
+    gemm_store_in<EPI>(a, row, col + 2, c.z, c.w, in[2]);
+    gemm_store_in<EPI>(a, row, col + 3, c.w, c.z, in[3]);
+  } else {
+    gemm_store<EPI>(a, row, col, c.x, c.y);
+    gemm_store<EPI>(a, row, col + 1, c.y, c.x);
+    gemm_store<EPI>(a, row, col + 2, c.z, c.w);
+    gemm_store<EPI>(a, row, col + 3, c.w, c.z);
+  }
 }
 
 // the K splits of gemm_mfma_kernel, added in split order, then the epilogue;
