@@ -96,6 +96,14 @@ __device__ __forceinline__ void store_kv(void *base, size_t idx, float v, int bf
     ((float *)base)[idx] = v;
 }
 
+// (u / n, u % n) for n > 0: shifts when n is a power of two (every head dim
+// in use; n is uniform, so the branch is too), a division otherwise
+__device__ __forceinline__ int2 divmod_n(int u, int n) {
+  if ((n & (n - 1)) == 0) return make_int2(u >> __builtin_ctz(n), u & (n - 1));
+  const int q = u / n;
+  return make_int2(q, u - q * n);
+}
+
 // Block-wide sum over 256 threads in a fixed order (wave partials, then 0..3).
 __device__ float block_sum(float v, float *scratch4) {
   v = group_sum<kWave>(v);
@@ -1113,7 +1121,8 @@ __device__ __forceinline__ void gemm_store(const GemmArgs &a, int row, int col, 
       if (col < a.q_dim + a.kv_dim) {
         const bool is_q = col < a.q_dim;
         const int rr = is_q ? col : col - a.q_dim;
-        const int u = rr >> 1, head = u / half, p = u - head * half;
+        const int2 hp = divmod_n(rr >> 1, half);
+        const int head = hp.x, p = hp.y;
         const float2 cs = a.rope[(size_t)pos * half + p];
         const float o0 = y0 * cs.x - y1 * cs.y;
         const float o1 = y1 * cs.x + y0 * cs.y;
@@ -1127,9 +1136,8 @@ __device__ __forceinline__ void gemm_store(const GemmArgs &a, int row, int col, 
           store_kv(a.kc, base + p + half, o1, a.kv_bf16);
         }
       } else {
-        const int rr = col - a.q_dim - a.kv_dim;
-        const int head = rr / d, j = rr - head * d;
-        const size_t base = ((size_t)head * a.max_seq + pos) * d + j;
+        const int2 hj = divmod_n(col - a.q_dim - a.kv_dim, d);
+        const size_t base = ((size_t)hj.x * a.max_seq + pos) * d + hj.y;
         store_kv(a.vc, base, y0, a.kv_bf16);
         store_kv(a.vc, base + 1, y1, a.kv_bf16);
       }
@@ -1146,21 +1154,20 @@ struct EpiIn {
 };
 template <int EPI>
 __device__ __forceinline__ EpiIn gemm_epi_load(const GemmArgs &a, int row, int col) {
+  // branch-free: a load under a divergent branch makes the compiler wait for
+  // it where the branch joins, one round trip per element. (row, col) must be
+  // in range; odd columns load their pair's values, which go unused.
   EpiIn in;
   in.u = make_float2(0.f, 0.f);
   in.v = make_float2(1.f, 0.f);
   if (EPI == EPI_RESID) {
     in.u.x = a.y[(size_t)row * a.N + col];
   } else if (EPI == EPI_QKV) {
-    if ((col & 1) == 0) {
-      in.u = make_float2(a.bias[col], a.bias[col + 1]);
-      if (col < a.q_dim + a.kv_dim) {
-        const int half = a.head_dim >> 1;
-        const int rr = col < a.q_dim ? col : col - a.q_dim;
-        const int u = rr >> 1, p = u - (u / half) * half;
-        in.v = a.rope[(size_t)(a.start_pos + row) * half + p];
-      }
-    }
+    const int ce = col & ~1, half = a.head_dim >> 1;
+    in.u = make_float2(a.bias[ce], a.bias[ce + 1]);
+    // v columns (past q and k) use no RoPE factor; any in-range one is read
+    const int rr = ce < a.q_dim ? ce : ce - a.q_dim;
+    in.v = a.rope[(size_t)(a.start_pos + row) * half + divmod_n(rr >> 1, half).y];
   }
   return in;
 }
@@ -1178,7 +1185,8 @@ __device__ __forceinline__ void gemm_store_in(const GemmArgs &a, int row, int co
       if (col < a.q_dim + a.kv_dim) {
         const bool is_q = col < a.q_dim;
         const int rr = is_q ? col : col - a.q_dim;
-        const int u = rr >> 1, head = u / half, p = u - head * half;
+        const int2 hp = divmod_n(rr >> 1, half);
+        const int head = hp.x, p = hp.y;
         const float2 cs = in.v;
         const float o0 = y0 * cs.x - y1 * cs.y;
         const float o1 = y1 * cs.x + y0 * cs.y;
@@ -1192,9 +1200,8 @@ __device__ __forceinline__ void gemm_store_in(const GemmArgs &a, int row, int co
           store_kv(a.kc, base + p + half, o1, a.kv_bf16);
         }
       } else {
-        const int rr = col - a.q_dim - a.kv_dim;
-        const int head = rr / d, j = rr - head * d;
-        const size_t base = ((size_t)head * a.max_seq + pos) * d + j;
+        const int2 hj = divmod_n(col - a.q_dim - a.kv_dim, d);
+        const size_t base = ((size_t)hj.x * a.max_seq + pos) * d + hj.y;
         store_kv(a.vc, base, y0, a.kv_bf16);
         store_kv(a.vc, base + 1, y1, a.kv_bf16);
       }
@@ -1336,6 +1343,100 @@ struct PfCfg {
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t pf_rsrc(const uint16_t *base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, (int)bytes, 0x00020000);
+}
+
+// gemm_pf_kernel's QKV epilogue (bias, RoPE, q / K / V stores) by column
+// pairs: lane pair index pi takes columns (2j, 2j + 1) of tile row pi / (BN/2)
+// from the accumulator tile cs in LDS, so every lane works; a batch of pairs'
+// bias and RoPE reads goes out before its stores. REG 0 / 1 / 2: a full tile
+// of q / k / v columns with power-of-two head dims (shifts, no bounds or
+// region tests; KB: bf16 cache); REG 3: any tile, every test per pair. Same
+// arithmetic as gemm_store<EPI_QKV> for each element.
+template <class C, int REG, bool KB>
+__device__ __forceinline__ void qkv_pairs(const GemmArgs &a, const float *cs, int tid, int m0, int n0) {
+  // one batch of up to 32 pairs: with one wave per SIMD nothing hides a
+  // batch's read latency, so the reads go out together
+  constexpr int HB = C::BN / 2, NIT2 = C::BM * HB / C::NTH;
+  constexpr int EB2 = NIT2 <= 32 ? NIT2 : (NIT2 % 8 == 0 ? 8 : 1);
+  static_assert(C::BM * HB % C::NTH == 0, "whole epilogue iterations");
+  const int M = a.M, N = a.N, d = a.head_dim, half = d >> 1, qd = a.q_dim, qkd = a.q_dim + a.kv_dim;
+  const int lh = __builtin_ctz(half), ld = lh + 1;
+  for (int it0 = 0; it0 < NIT2; it0 += EB2) {
+    float2 bv[EB2], rv[EB2];
+#pragma unroll
+    for (int e = 0; e < EB2; e++) {
+      const int pi = tid + (it0 + e) * C::NTH;
+      const int row = REG < 3 ? m0 + pi / HB : min(m0 + pi / HB, M - 1);
+      const int col = REG < 3 ? n0 + 2 * (pi % HB) : min(n0 + 2 * (pi % HB), N - 2);
+      bv[e] = make_float2(a.bias[col], a.bias[col + 1]);
+      if (REG == 0 || REG == 1) {
+        const int rr = REG == 0 ? col : col - qd;
+        rv[e] = a.rope[(size_t)(a.start_pos + row) * half + ((rr >> 1) & (half - 1))];
+      } else if (REG == 3) {
+        const int rr = col < qd ? col : col - qd;  // v columns read an unused factor
+        rv[e] = a.rope[(size_t)(a.start_pos + row) * half + divmod_n(rr >> 1, half).y];
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < EB2; e++) {
+      const int pi = tid + (it0 + e) * C::NTH;
+      const int tr = pi / HB, tc = 2 * (pi % HB);
+      const int row = m0 + tr, col = n0 + tc;
+      if (REG == 3 && !(row < M && col < N)) continue;
+      const float2 yv = *(const float2 *)(cs + tr * C::BN + tc);
+      const float y0 = yv.x + bv[e].x, y1 = yv.y + bv[e].y;
+      const int pos = a.start_pos + row;
+      if (REG == 0) {
+        const int u = col >> 1;
+        const float o0 = y0 * rv[e].x - y1 * rv[e].y;
+        const float o1 = y1 * rv[e].x + y0 * rv[e].y;
+        float *qr = a.q_out + (size_t)row * qd + ((u >> lh) << ld) + (u & (half - 1));
+        qr[0] = o0;
+        qr[half] = o1;
+      } else if (REG == 1) {
+        const int u = (col - qd) >> 1;
+        const float o0 = y0 * rv[e].x - y1 * rv[e].y;
+        const float o1 = y1 * rv[e].x + y0 * rv[e].y;
+        const size_t base = ((size_t)(u >> lh) * a.max_seq + pos) * d + (u & (half - 1));
+        if (KB) {
+          ((uint16_t *)a.kc)[base] = f2bf(o0);
+          ((uint16_t *)a.kc)[base + half] = f2bf(o1);
+        } else {
+          ((float *)a.kc)[base] = o0;
+          ((float *)a.kc)[base + half] = o1;
+        }
+      } else if (REG == 2) {
+        const int rr = col - qkd;
+        const size_t base = ((size_t)(rr >> ld) * a.max_seq + pos) * d + (rr & (d - 1));
+        if (KB) {
+          *(uint32_t *)((uint16_t *)a.vc + base) = (uint32_t)f2bf(y0) | ((uint32_t)f2bf(y1) << 16);
+        } else {
+          *(float2 *)((float *)a.vc + base) = make_float2(y0, y1);
+        }
+      } else {
+        if (col < qkd) {
+          const bool is_q = col < qd;
+          const int2 hp = divmod_n((is_q ? col : col - qd) >> 1, half);
+          const float o0 = y0 * rv[e].x - y1 * rv[e].y;
+          const float o1 = y1 * rv[e].x + y0 * rv[e].y;
+          if (is_q) {
+            float *qr = a.q_out + (size_t)row * qd + hp.x * d + hp.y;
+            qr[0] = o0;
+            qr[half] = o1;
+          } else {
+            const size_t base = ((size_t)hp.x * a.max_seq + pos) * d + hp.y;
+            store_kv(a.kc, base, o0, a.kv_bf16);
+            store_kv(a.kc, base + half, o1, a.kv_bf16);
+          }
+        } else {
+          const int2 hj = divmod_n(col - qkd, d);
+          const size_t base = ((size_t)hj.x * a.max_seq + pos) * d + hj.y;
+          store_kv(a.vc, base, y0, a.kv_bf16);
+          store_kv(a.vc, base + 1, y1, a.kv_bf16);
+        }
+      }
+    }
+  }
 }
 
 template <class C, int EPI>
@@ -1513,6 +1614,25 @@ __global__ void __launch_bounds__(C::NTH) gemm_pf_kernel(GemmArgs a) {
     }
     return;
   }
+  if constexpr (EPI == EPI_QKV) {
+    // Decisions that are uniform for the tile are taken once here: a full
+    // tile whose columns are all q, all k or all v, with power-of-two head
+    // dims, runs a branch-free pair loop (see qkv_pairs).
+    const int half = a.head_dim >> 1, qd = a.q_dim, qkd = a.q_dim + a.kv_dim;
+    const bool fast = (half & (half - 1)) == 0 && m0 + C::BM <= M && n0 + C::BN <= N;
+    const int reg = !fast ? 3 : n0 + C::BN <= qd ? 0 : (n0 >= qd && n0 + C::BN <= qkd) ? 1 : n0 >= qkd ? 2 : 3;
+    const bool kb = a.kv_bf16 != 0;
+    switch (reg * 2 + (kb ? 1 : 0)) {
+      case 0: qkv_pairs<C, 0, false>(a, cs, tid, m0, n0); break;
+      case 1: qkv_pairs<C, 0, true>(a, cs, tid, m0, n0); break;
+      case 2: qkv_pairs<C, 1, false>(a, cs, tid, m0, n0); break;
+      case 3: qkv_pairs<C, 1, true>(a, cs, tid, m0, n0); break;
+      case 4: qkv_pairs<C, 2, false>(a, cs, tid, m0, n0); break;
+      case 5: qkv_pairs<C, 2, true>(a, cs, tid, m0, n0); break;
+      default: qkv_pairs<C, 3, false>(a, cs, tid, m0, n0); break;
+    }
+    return;
+  }
   // the epilogues that read global memory: a batch of EB elements' reads
   // first, then their stores
   constexpr int NIT = C::BM * C::BN / C::NTH, EB = NIT % 8 == 0 ? 8 : 1;
@@ -1523,7 +1643,7 @@ __global__ void __launch_bounds__(C::NTH) gemm_pf_kernel(GemmArgs a) {
     for (int e = 0; e < EB; e++) {
       const int idx = tid + (it0 + e) * C::NTH;
       const int row = m0 + idx / C::BN, col = n0 + idx % C::BN;
-      if (row < M && col < N) in[e] = gemm_epi_load<EPI>(a, row, col);
+      in[e] = gemm_epi_load<EPI>(a, min(row, M - 1), min(col, N - 1));  // clamped, unconditional
     }
 #pragma unroll
     for (int e = 0; e < EB; e++) {
