@@ -1602,6 +1602,21 @@ __global__ void __launch_bounds__(C::NTH) gemm_pf_kernel(GemmArgs a) {
   __syncthreads();
   const bool split = S > 1;
   float *ws = a.ws + (size_t)z * M * N;
+  if (EPI == EPI_GU && !split) {
+    // h = silu(gate) * up by column pairs (gate 2j, up 2j + 1), one pair per
+    // lane: every lane works and consecutive lanes write consecutive h
+    constexpr int HB = C::BN / 2;
+    for (int pi = tid; pi < C::BM * HB; pi += C::NTH) {
+      const int tr = pi / HB, tc = 2 * (pi % HB);
+      const int row = m0 + tr, col = n0 + tc;
+      if (row < M && col < N) {
+        const float2 gu = *(const float2 *)(cs + tr * C::BN + tc);
+        const size_t o = (size_t)row * (N >> 1) + (col >> 1);
+        split2(silu(gu.x) * gu.y, a.h_hi + o, a.h_lo + o);
+      }
+    }
+    return;
+  }
   if (split || EPI == EPI_STORE || EPI == EPI_GU) {
     for (int idx = tid; idx < C::BM * C::BN; idx += C::NTH) {
       const int tr = idx / C::BN, tc = idx % C::BN;
