@@ -2358,16 +2358,16 @@ __global__ void __launch_bounds__(256) attn_prefill_merge_kernel(AttnPrefillArgs
   const int h = (int)(qh % a.nq), q = (int)(qh / a.nq);
   const size_t zs = (size_t)a.M * (kFaD + 2);  // one split's partials of a head
   const float *p = a.part + (size_t)h * ns * zs + (size_t)q * (kFaD + 2);
-  // every split's (max, sum) and outputs in one round trip (ns <= 4)
+  // every split's (max, sum) and outputs in one round trip (ns <= 4); the
+  // loads are unconditional (split min(z, ns - 1) for z >= ns, unused): a
+  // load under a branch would be waited for where the branch joins
   float2 ml[4], x0[4], x1[4];
 #pragma unroll
   for (int z = 0; z < 4; z++) {
-    if (z < ns) {
-      const float *pz = p + z * zs;
-      ml[z] = *(const float2 *)(pz + kFaD);
-      x0[z] = *(const float2 *)(pz + 4 * d4);
-      x1[z] = *(const float2 *)(pz + 4 * d4 + 2);
-    }
+    const float *pz = p + min(z, ns - 1) * zs;
+    ml[z] = *(const float2 *)(pz + kFaD);
+    x0[z] = *(const float2 *)(pz + 4 * d4);
+    x1[z] = *(const float2 *)(pz + 4 * d4 + 2);
   }
   float mmax = -INFINITY;
 #pragma unroll
