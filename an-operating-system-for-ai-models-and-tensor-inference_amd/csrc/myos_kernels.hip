@@ -2679,9 +2679,12 @@ using PfT256 = PfCfg<2, 4, 2, 2>;
 // 128 x 256 with eight waves (two per SIMD, 64 x 64 each): one wave's MFMAs
 // run while the other waits on LDS, which the four-wave 128 x 256 tile cannot
 using PfW256 = PfCfg<2, 2, 2, 4>;
-constexpr int kPfCfgs = 5;
-constexpr int kPfPlanCfgs = 4;  // the cost model's candidates (PfW256 is picked by shape)
-constexpr int kPfBN[kPfCfgs] = {PfT32::BN, PfT64::BN, PfT128::BN, PfT256::BN, PfW256::BN};
+// 128 x 192 with eight waves (32 x 96 each): 8 N tiles of a 1536-wide
+// projection, so 16 M tiles x 2 splits fill the 256 CUs exactly
+using PfW192 = PfCfg<1, 3, 4, 2>;
+constexpr int kPfCfgs = 6;
+constexpr int kPfPlanCfgs = 4;  // the cost model's candidates (the wider ones are picked by shape)
+constexpr int kPfBN[kPfCfgs] = {PfT32::BN, PfT64::BN, PfT128::BN, PfT256::BN, PfW256::BN, PfW192::BN};
 constexpr int kCUs = 256;
 
 int g_force_cfg = -1, g_force_splits = 0;
@@ -2717,7 +2720,11 @@ GemmPlan pf_plan(int M, int N, int K) {
     return best;
   }
   if (M > 256 && N <= 4096 && K >= 4096) {
-    best.cfg = 4;
+    // the 128 x 192 tile when its two-split grid fits the CUs in one round
+    // (down at 2048 rows: 256 workgroups, 139 -> 121 us against 192 of the
+    // 128 x 256 tile)
+    const long t192 = ((M + 127) / 128) * (long)(N / 192);
+    best.cfg = N % 192 == 0 && 2 * t192 <= kCUs ? 5 : 4;
     best.splits = 2;
     return best;
   }
@@ -2809,6 +2816,7 @@ static hipError_t go_pf_cfg(const GemmArgs &a, int cfg, int splits, hipStream_t 
     case 2: return go_pf<PfT128, EPI>(a, splits, s);
     case 3: return go_pf<PfT256, EPI>(a, splits, s);
     case 4: return go_pf<PfW256, EPI>(a, splits, s);
+    case 5: return go_pf<PfW192, EPI>(a, splits, s);
     default: return hipErrorInvalidValue;
   }
 }
