@@ -394,6 +394,7 @@ struct orc_model {
   orc_shape s;
   size_t max_seq, len, q_dim, kv_dim;
   int threads;
+  int kv_bf16; /* cache holds bf16 values (RNE on store); every attention read sees them */
   orc_layer *layers;
   const uint16_t *embed, *final_norm, *head;
   /* kv_cache.rs:89-125: [layer][kv_head][max_seq][head_dim] f32, zeroed */
@@ -476,13 +477,42 @@ int orc_kv_read(const orc_model *m, size_t layer, size_t head, size_t pos, float
   return ORC_OK;
 }
 
-/* KvCache::store_at, kv_cache.rs:158-183 */
+/* f32 -> nearest bf16 (ties to even), widened back to f32; NaN stays a quiet
+ * NaN. The reference's cache is f32 (kv_cache.rs:93-94); this is the value a
+ * bf16 cache slot holds. */
+float orc_round_bf16(float x) {
+  uint32_t u;
+  memcpy(&u, &x, 4);
+  if ((u & 0x7fffffffu) > 0x7f800000u)
+    u = (u | 0x00400000u) & 0xffff0000u;
+  else
+    u = (u + 0x7fffu + ((u >> 16) & 1u)) & 0xffff0000u;
+  float r;
+  memcpy(&r, &u, 4);
+  return r;
+}
+
+static void round_bf16_n(float *x, size_t n) {
+  for (size_t i = 0; i < n; i++) x[i] = orc_round_bf16(x[i]);
+}
+
+int orc_set_kv_bf16(orc_model *m, int on) {
+  if (m->len) return ORC_E_KV_RANGE; /* only while the cache is empty */
+  m->kv_bf16 = on != 0;
+  return ORC_OK;
+}
+
+/* KvCache::store_at, kv_cache.rs:158-183 (rounded to bf16 in the bf16 mode) */
 static void kv_store(orc_model *m, size_t layer, size_t pos, const float *k, const float *v) {
   size_t d = m->s.head_dim;
   for (size_t h = 0; h < m->s.num_kv_heads; h++) {
     size_t o = kv_off(m, layer, h, pos);
     memcpy(m->kc + o, k + h * d, d * sizeof(float));
     memcpy(m->vc + o, v + h * d, d * sizeof(float));
+    if (m->kv_bf16) {
+      round_bf16_n(m->kc + o, d);
+      round_bf16_n(m->vc + o, d);
+    }
   }
 }
 
@@ -528,6 +558,10 @@ static void attention_layer(orc_model *m, size_t layer, size_t pos) {
   orc_add_bf16_bias(m->v, L->bv, kd);
   orc_rope_f32_inplace(m->q, qd, (uint32_t)pos, m->s.head_dim, m->s.rope_theta);
   orc_rope_f32_inplace(m->k, kd, (uint32_t)pos, m->s.head_dim, m->s.rope_theta);
+  if (m->kv_bf16) { /* the token's own row as its cache slot will hold it */
+    round_bf16_n(m->k, kd);
+    round_bf16_n(m->v, kd);
+  }
   kv_pack_with_token(m, layer, pos);
   orc_gqa_attn_f32(m->att, m->q, m->pack_k, m->pack_v, m->probs, m->s.num_q_heads,
                    m->s.num_kv_heads, m->s.head_dim, pos + 1, 0, 0);
@@ -617,6 +651,15 @@ int orc_prefill(orc_model *m, const uint32_t *tokens, size_t n) {
   float *X = zalloc(n * H), *N = zalloc(n * H), *Q = zalloc(n * qd), *K = zalloc(n * kd);
   float *V = zalloc(n * kd), *A = zalloc(n * qd), *P = zalloc(n * H), *G = zalloc(n * I);
   float *U = zalloc(n * I), *F = zalloc(n * I);
+  {
+    float *bufs[] = {X, N, Q, K, V, A, P, G, U, F};
+    int bad = 0;
+    for (size_t i = 0; i < 10; i++) bad |= bufs[i] == NULL;
+    if (bad) {
+      for (size_t i = 0; i < 10; i++) free(bufs[i]);
+      return ORC_E_NOMEM;
+    }
+  }
   for (size_t i = 0; i < n; i++) orc_embed_gather_bf16(X + i * H, m->embed, m->s.vocab, H, tokens[i]);
   for (size_t l = 0; l < m->s.num_layers; l++) {
     const orc_layer *L = &m->layers[l];
@@ -639,6 +682,11 @@ int orc_prefill(orc_model *m, const uint32_t *tokens, size_t n) {
     {
       int parts = n < 8 ? 1 : m->threads;
       attend_job job = {m, A, Q, n, start, end, zalloc((size_t)parts * end)};
+      if (!job.probs) {
+        float *bufs[] = {X, N, Q, K, V, A, P, G, U, F};
+        for (size_t i = 0; i < 10; i++) free(bufs[i]);
+        return ORC_E_NOMEM;
+      }
       pool_run(attend_part, &job, parts);
       free(job.probs);
     }

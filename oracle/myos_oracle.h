@@ -43,6 +43,7 @@ enum {
   ORC_E_POSITION = 4,
   ORC_E_KV_FULL = 5,
   ORC_E_KV_RANGE = 6,
+  ORC_E_NOMEM = 7, /* a scratch allocation failed (no reference counterpart) */
 };
 
 float orc_bf16_to_f32(uint16_t bits);
@@ -96,6 +97,13 @@ const float *orc_hidden(const orc_model *m);  /* residual stream after the last 
 const float *orc_normed(const orc_model *m);  /* final-norm output fed to the head */
 int orc_kv_read(const orc_model *m, size_t layer, size_t head, size_t pos, float *k, float *v);
 void orc_set_threads(orc_model *m, int threads);
+/* bf16 KV cache mode (the reference's cache is f32, kv_cache.rs:93-94): every
+ * K/V value is rounded to bf16 (nearest, ties to even) when stored, and the
+ * decode step's own row is rounded the same way before attention, so every
+ * attention read sees the value a bf16 cache slot holds. Only while the cache
+ * is empty (ORC_E_KV_RANGE otherwise). */
+int orc_set_kv_bf16(orc_model *m, int on);
+float orc_round_bf16(float x);
 int orc_attention_layer(orc_model *m, size_t layer, size_t pos, float *residual,
                         const float *proj_in);
 int orc_kv_advance(orc_model *m);

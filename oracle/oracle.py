@@ -92,6 +92,9 @@ def _declare(L):
     L.orc_set_threads.restype = None
     L.orc_attention_layer.argtypes = [P, SZ, SZ, P, P]
     L.orc_kv_advance.argtypes = [P]
+    L.orc_set_kv_bf16.argtypes = [P, C.c_int]
+    L.orc_round_bf16.argtypes = [C.c_float]
+    L.orc_round_bf16.restype = C.c_float
 
 
 def _p(a: np.ndarray):
@@ -111,6 +114,11 @@ def bf16_bits_exact(values) -> np.ndarray:
     b = f32(values).view(np.uint32)
     assert np.all(b & 0xFFFF == 0), "value not exact in bf16"
     return (b >> 16).astype(np.uint16)
+
+
+def round_bf16(x) -> np.float32:
+    """The value a bf16 KV-cache slot holds for f32 x (nearest, ties to even)."""
+    return np.float32(lib().orc_round_bf16(np.float32(x)))
 
 
 def bf16_to_f32(bits) -> np.ndarray:
@@ -204,7 +212,8 @@ def greedy_token(logits):
 class Model:
     """Oracle model over a dict of BF16 bit arrays keyed by qwen25_layout names."""
 
-    def __init__(self, shape: dict, tensors: dict, max_seq: int, threads: int = 8):
+    def __init__(self, shape: dict, tensors: dict, max_seq: int, threads: int = 8,
+                 kv_bf16: bool = False):
         self._keep = []
         self.shape = dict(shape)
         s = Shape(**{k: shape[k] for k, _ in Shape._fields_})
@@ -234,6 +243,8 @@ class Model:
                                      None if head is None else head.ctypes.data, threads)
         if not self.h:
             raise ValueError("oracle rejected the shape")
+        if kv_bf16:
+            assert lib().orc_set_kv_bf16(self.h, 1) == 0
 
     def __del__(self):
         if getattr(self, "h", None):

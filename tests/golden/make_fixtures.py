@@ -10,8 +10,12 @@ against:
 * qwen25_1_5b_long.npz -- Qwen2.5-1.5B shape, random-init seed 0 (the
   bench's weights), 2048 seeded uniform prompt ids prefilled, then 256
   greedy decode steps (max_seq 2304), f32 KV cache;
+* qwen25_1_5b_long_bf16kv.npz -- the same workload with the bf16 KV cache:
+  the oracle's bf16 mode rounds every K/V value to bf16 (nearest, ties to
+  even) when it is stored and the decode step's own row the same way;
 * qwen25_7b_s1.npz -- Qwen2.5-7B shape (untied lm_head), seed 0, 128
-  seeded prompt ids, then 8 greedy steps.
+  seeded prompt ids, then 128 greedy steps (greedy_decode,
+  qwen25_block.rs:765-780).
 
 Each holds the prompt, the logits / final hidden / normed vector after the
 prefill and after the last step, every step's greedy id with its top-1 /
@@ -20,7 +24,7 @@ sampled fingerprint of the weights file so a test can check it regenerated
 the same bytes. Inputs come from the library's seeded writer
 (myos_write_random_qwen25); every expected value comes from the oracle.
 
-usage: python tests/golden/make_fixtures.py [long|7b|all] [--threads N]
+usage: python tests/golden/make_fixtures.py [long|long_bf16|7b|all] [--threads N]
 """
 from __future__ import annotations
 
@@ -68,9 +72,10 @@ def topk(lg):
     return idx.astype(np.uint32), lg[idx].astype(np.float32)
 
 
-def run(name, preset, n_prompt, n_steps, kv_points, threads, workdir):
+def run(name, preset, n_prompt, n_steps, kv_points, threads, workdir, kv_bf16=False,
+        weights=None):
     shape = myos.preset(preset)
-    path = os.path.join(workdir, f"{name}_seed0.safetensors")
+    path = os.path.join(workdir, f"{weights or name}_seed0.safetensors")
     if not os.path.exists(path):
         t0 = time.time()
         myos.write_random_qwen25(path, shape, seed=0, std=0.02, threads=threads)
@@ -80,7 +85,7 @@ def run(name, preset, n_prompt, n_steps, kv_points, threads, workdir):
                    shape.rope_theta)
     t = oracle.load_safetensors_bits(path)
     max_seq = n_prompt + n_steps
-    m = oracle.Model(s, t, max_seq, threads=threads)
+    m = oracle.Model(s, t, max_seq, threads=threads, kv_bf16=kv_bf16)
     prompt = np.random.default_rng(PROMPT_SEED).integers(0, shape.vocab, n_prompt).astype(np.uint32)
     t0 = time.time()
     assert m.prefill(prompt) == 0
@@ -112,6 +117,7 @@ def run(name, preset, n_prompt, n_steps, kv_points, threads, workdir):
                 kv[a, b, c, 0], kv[a, b, c, 1] = m.kv(l, h, p)
     out.update(kv=kv, kv_layers=np.array(layers), kv_heads=np.array(heads),
                kv_positions=np.array(positions), max_seq=np.array(max_seq),
+               kv_bf16=np.array(bool(kv_bf16)),
                weights_fingerprint=np.array(file_fingerprint(path)),
                shape=np.array([shape.hidden, shape.num_q_heads, shape.num_kv_heads,
                                shape.head_dim, shape.intermediate, shape.vocab,
@@ -124,7 +130,7 @@ def run(name, preset, n_prompt, n_steps, kv_points, threads, workdir):
 
 def main():
     ap = argparse.ArgumentParser()
-    ap.add_argument("which", nargs="?", default="all", choices=["long", "7b", "all"])
+    ap.add_argument("which", nargs="?", default="all", choices=["long", "long_bf16", "7b", "all"])
     ap.add_argument("--threads", type=int, default=os.cpu_count() or 8)
     ap.add_argument("--workdir", default="/tmp/myos_fixtures")
     a = ap.parse_args()
@@ -132,9 +138,13 @@ def main():
     if a.which in ("long", "all"):
         run("qwen25_1_5b_long", myos.SHAPE_QWEN25_1_5B, 2048, 256,
             ([0, 13, 27], [0, 1], [0, 1023, 2047, 2048, 2175, 2303]), a.threads, a.workdir)
+    if a.which in ("long_bf16", "all"):
+        run("qwen25_1_5b_long_bf16kv", myos.SHAPE_QWEN25_1_5B, 2048, 256,
+            ([0, 13, 27], [0, 1], [0, 1023, 2047, 2048, 2175, 2303]), a.threads, a.workdir,
+            kv_bf16=True, weights="qwen25_1_5b_long")
     if a.which in ("7b", "all"):
-        run("qwen25_7b_s1", myos.SHAPE_QWEN25_7B, 128, 8,
-            ([0, 27], [0, 3], [0, 127, 128, 135]), a.threads, a.workdir)
+        run("qwen25_7b_s1", myos.SHAPE_QWEN25_7B, 128, 128,
+            ([0, 13, 27], [0, 3], [0, 127, 128, 191, 255]), a.threads, a.workdir)
 
 
 if __name__ == "__main__":

@@ -133,6 +133,22 @@ def two_layer_fixture():
     return fixture_shape(2), t
 
 
+def bf16_kv_fixture():
+    """The block fixture's shape with a value projection whose outputs are
+    not bf16 values: token 0 normalises to [1, 1], so v = [1 + 3 * 2^-8,
+    1 + 2^-9] exactly in f32, and a bf16 cache slot rounds them (nearest,
+    ties to even) to [1 + 2^-6, 1]. q = k = 0, so attention weights every
+    position equally; o_proj copies head 0's output into the stream and the
+    MLP is zero, so the hidden state after the layer is [1, 1] + attention."""
+    t = fixture_embed_and_final()
+    p = "model.layers.0."
+    block_fixture_layer(t, 0, [0.0] * 4, [0.0, 0.0],
+                        [1.0, 0.0, 0.0, 0.0, 0.0, 1.0, 0.0, 0.0], [0.0] * 4, [0.0] * 4,
+                        [0.0] * 4)
+    t[p + "self_attn.v_proj.weight"] = bits([1.0, 3.0 * 2.0 ** -8, 1.0, 2.0 ** -9], (2, 2))
+    return fixture_shape(), t
+
+
 # ------------------------------------------------------------- rich map ----
 
 _PAT = np.array([0.5, -0.25, 1.0, 0.0, -1.0, 0.125, 2.0, -0.5], np.float32)

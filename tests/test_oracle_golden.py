@@ -598,6 +598,94 @@ def test_chunk_prefill_equals_serial(orc):
     assert _kv_bits(mc, w, 33) == _kv_bits(ms, w, 33)
 
 
+# -------------------------------------------------- bf16 KV cache mode ----
+# The reference's cache is f32 (kv_cache.rs:93-94). The bf16 variant the
+# long-context workload names rounds every K/V value to bf16 (nearest, ties
+# to even) when it is stored, and the decode step's own row the same way, so
+# attention always reads the values a bf16 slot holds.
+
+def test_round_bf16_closed_forms(orc):
+    r = lambda x: float(orc.round_bf16(np.float32(x)))
+    for x in (1.0, -2.5, 0.0, 2.0 ** -126, 3.0 * 2.0 ** 100, 1.0 + 2.0 ** -7):
+        assert r(x) == x  # exactly representable values survive
+    assert r(1.0 + 2.0 ** -8) == 1.0                      # tie -> even (mantissa 0)
+    assert r(1.0 + 3.0 * 2.0 ** -8) == 1.0 + 2.0 ** -6    # tie -> even (mantissa 2)
+    assert r(-(1.0 + 3.0 * 2.0 ** -8)) == -(1.0 + 2.0 ** -6)
+    assert r(1.0 + 2.0 ** -8 + 2.0 ** -20) == 1.0 + 2.0 ** -7  # above half
+    assert r(1.0 + 2.0 ** -9) == 1.0                      # below half
+    assert r(np.inf) == np.inf and r(-np.inf) == -np.inf
+    assert math.isnan(r(np.nan))
+    assert r(np.finfo(np.float32).max) == np.inf           # rounds past the largest bf16
+    assert r(2.0 ** -140) == 0.0                           # a denormal below half the smallest bf16 step
+
+
+def test_bf16_kv_closed_form(orc):
+    # bf16_kv_fixture: v = [1 + 3 2^-8, 1 + 2^-9] rounds to [1 + 2^-6, 1].
+    from model_fixtures import bf16_kv_fixture
+    s, t = bf16_kv_fixture()
+    v32 = [1.0 + 3.0 * 2.0 ** -8, 1.0 + 2.0 ** -9]
+    v16 = [1.0 + 2.0 ** -6, 1.0]
+    for bf16, v in ((False, v32), (True, v16)):
+        m = orc.Model(s, t, 4, threads=1, kv_bf16=bf16)
+        assert m.forward_token(0, 0) == 0
+        # one position: the step's own row, as its slot holds it
+        assert [float(x) for x in m.hidden()] == [1.0 + v[0], 1.0 + v[1]], bf16
+        assert [float(x) for x in m.kv(0, 0, 0)[1]] == v
+        # two positions weighted 1/2 each: the cached row and the step's row
+        assert m.forward_token(0, 1) == 0
+        assert [float(x) for x in m.hidden()] == [1.0 + v[0], 1.0 + v[1]], bf16
+        # chunk prefill reads the chunk's rows back from the cache: the same
+        p = orc.Model(s, t, 4, threads=1, kv_bf16=bf16)
+        assert p.prefill([0, 0]) == 0
+        assert fbits(p.hidden()) == fbits(m.hidden())
+    m = orc.Model(s, t, 4, threads=1, kv_bf16=True)
+    assert m.forward_token(0, 0) == 0
+    assert orc.lib().orc_set_kv_bf16(m.h, 0) == 6  # only while the cache is empty
+
+
+def test_bf16_kv_layer0_rows_are_rne_of_f32(orc):
+    # Layer 0's K/V depend only on the prompt's embeddings, so the bf16 mode's
+    # rows must be the f32 mode's rows rounded by an independent RNE.
+    from model_fixtures import random_map, rne_bf16, shape_dict
+    s = shape_dict(64, 4, 2, 16, 96, 50, 2, 1e-6)
+    t = random_map(s, seed=5, std=0.3)
+    f, b = orc.Model(s, t, 8, threads=2), orc.Model(s, t, 8, threads=2, kv_bf16=True)
+    prompt = [3, 17, 41, 8, 22]
+    assert f.prefill(prompt) == 0 and b.prefill(prompt) == 0
+    assert b.forward_token(9, 5) == 0 and f.forward_token(9, 5) == 0
+    changed = 0
+    for h in range(2):
+        for p in range(6):
+            kf, vf = f.kv(0, h, p)
+            kb, vb = b.kv(0, h, p)
+            want_k = (rne_bf16(kf).astype(np.uint32) << 16).view(np.float32)
+            want_v = (rne_bf16(vf).astype(np.uint32) << 16).view(np.float32)
+            assert fbits(kb) == fbits(want_k) and fbits(vb) == fbits(want_v), (h, p)
+            changed += int(np.sum(kb != kf)) + int(np.sum(vb != vf))
+    assert changed > 0.9 * 2 * 6 * 2 * 16  # almost every value moved
+    # later layers read rounded rows, so their results move too
+    assert fbits(b.kv(1, 0, 5)[0]) != fbits((rne_bf16(f.kv(1, 0, 5)[0]).astype(np.uint32) << 16)
+                                            .view(np.float32))
+
+
+def test_bf16_kv_chunk_prefill_equals_serial(orc):
+    # With every attention read taken from the cache's values, chunk prefill
+    # and serial decode stay bit-identical in the bf16 mode too.
+    s = rich_shape(2)
+    t = rich_map(s)
+    from model_fixtures import random_map, shape_dict
+    for s, t in ((s, t), (shape_dict(32, 4, 2, 8, 48, 40, 2, 1e-6), None)):
+        if t is None:
+            t = random_map(s, seed=9, std=0.3)
+        ms = orc.Model(s, t, 16, threads=2, kv_bf16=True)
+        mc = orc.Model(s, t, 16, threads=3, kv_bf16=True)
+        prompt = [1, 3, 0, 4, 2, 3, 1]
+        serial = _serial(ms, prompt, 0)
+        assert mc.prefill(prompt) == 0
+        assert fbits(mc.logits()) == fbits(serial)
+        assert _kv_bits(mc, s, 7) == _kv_bits(ms, s, 7)
+
+
 # ----------------------------------------------------- attn_wire.rs ----
 
 def _attn_model(orc, hidden, nq, nkv, d, proj, layers=1, max_seq=4):

@@ -2,7 +2,9 @@
 
 Each case copies oracle/myos_oracle.c to a temporary directory, plants one
 wiring mistake (MLP fed the pre-attention norm, a dropped residual, a layer's
-K/V written to another layer's slots, the untied head ignored, RoPE on V),
+K/V written to another layer's slots, the untied head ignored, RoPE on V, and
+in the bf16 KV mode: the step's own row left unrounded, truncation for
+round-to-nearest-even, V left unrounded),
 compiles it with the oracle's own flags and runs the composition pins of
 test_oracle_golden.py on it. At least one pin has to fail for every mistake.
 CPU only: nothing here touches the product library or a GPU.
@@ -30,6 +32,10 @@ MUTATIONS = {
     "untied_head_ignored": ("m->head = lm_head ? lm_head : embed;", "m->head = embed;"),
     "prefill_attends_layer0_cache": ("kv_pack(m, l, end);", "kv_pack(m, 0, end);"),
     "decode_rope_on_v": ("orc_rope_f32_inplace(m->k, kd,", "orc_rope_f32_inplace(m->v, kd,"),
+    "bf16_kv_step_row_unrounded": ("    round_bf16_n(m->k, kd);\n    round_bf16_n(m->v, kd);\n", ""),
+    "bf16_kv_truncates": ("u = (u + 0x7fffu + ((u >> 16) & 1u)) & 0xffff0000u;",
+                          "u = u & 0xffff0000u;"),
+    "bf16_kv_rounds_k_only": ("      round_bf16_n(m->vc + o, d);\n", ""),
 }
 
 PINS = [
@@ -40,6 +46,9 @@ PINS = [
     golden.test_untied_head_copy_equals_tied,
     golden.test_chunk_prefill_equals_serial,
     golden.test_attn_rope_k_not_v,
+    golden.test_round_bf16_closed_forms,
+    golden.test_bf16_kv_closed_form,
+    golden.test_bf16_kv_layer0_rows_are_rne_of_f32,
 ] + [lambda orc, d=d, s=s: golden.test_oracle_matches_textbook_forward(orc, d, s)
      for d, s in [((32, 4, 2, 8, 48, 40, 3), 1), ((64, 4, 4, 16, 80, 50, 4), 3)]]
 
