@@ -57,6 +57,9 @@ hipError_t launch_attn_decode(const AttnDecodeArgs &a, hipStream_t s);
 
 // ---- small ops --------------------------------------------------------------
 hipError_t launch_fill_zero(float *y, size_t n, hipStream_t s);
+// recompute NaN outputs of Y[batch, m] = X W^T as the reference's f32 chain
+hipError_t launch_gemm_nan_repair(float *y, const uint16_t *w, const float *x, int batch, int m, int k,
+                                  hipStream_t s);
 hipError_t launch_add_bias(float *y, const uint16_t *b, size_t n, hipStream_t s);
 hipError_t launch_embed_gather(float *out, const uint16_t *table, size_t hidden,
                                const uint32_t *token_dev, uint32_t token_host, hipStream_t s);
@@ -201,6 +204,7 @@ constexpr int kWFlagStride = 16;
 int persist_grid();                       // workgroups per launch
 int persist_tags_per_step(int layers);
 size_t persist_part_words(int nq, int max_seq, int d);
+size_t persist_pr_words(int H, int nq);
 bool persist_supported(int H, int I, int qdim, int d, int gq);
 bool persist_device_ok(const PersistArgs &a);  // shape, LDS and the current device fit
 hipError_t launch_decode_persistent(const PersistArgs &a, hipStream_t s);

@@ -439,8 +439,7 @@ int setup_persistent(myos_model *m) {
   // kernel's f32 buffers and barrier flags (none without it), the error word
   size_t words[8] = {m->q_dim, 2 * m->kv_dim, persist_part_words(a.nq, a.max_seq, a.d),
                      m->q_dim, s.hidden, s.hidden, 2 * (size_t)persist_grid(),
-                     (size_t)persist_grid() * persist_grid() *
-                         ((s.hidden + persist_grid() - 1) / persist_grid())};
+                     persist_pr_words((int)s.hidden, (int)s.num_q_heads)};
   if (!reg)
     for (size_t &w : words) w = 0;
   const size_t wide_f = wide ? wide_buffer_floats(a.H, a.I, a.nq, a.d, a.max_seq) : 0;

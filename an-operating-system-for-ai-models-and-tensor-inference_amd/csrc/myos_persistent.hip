@@ -329,6 +329,13 @@ __device__ __forceinline__ void seg_sum_n(float (&v)[N], int S) {
 __device__ __forceinline__ bool seg_leader(int lane, int S) {
   return (lane & (S - 1)) == (S == 32 ? 16 : 0);
 }
+// wave_sum of N values at once (the DPP steps overlap); lane 63 holds the totals
+template <int N>
+__device__ __forceinline__ void wave_sum_n(float (&v)[N]) {
+  seg_sum_n<N>(v, 32);
+#pragma unroll
+  for (int i = 0; i < N; i++) v[i] += dpp<0x143, 0xC>(v[i], 0.f);
+}
 
 // this lane's chunks of x (chunk lane + 64 i, 8 floats each) in registers,
 // read from LDS once for every row a phase multiplies
@@ -502,9 +509,18 @@ __device__ __forceinline__ void kvstore(uint8_t *base, size_t idx, float v) {
 // pairs of down. The workgroups that run no attention item (the first
 // nkv * nchmax) and no merge (the last nq) take them when they can hold
 // them: the attention chain's workgroups then carry almost no weight loads
-// into their waits. Otherwise every workgroup takes a share. Returns np.
-__host__ __device__ inline int gu_share(int I, int nkv, int nchmax, int nq, int *gst, int *gen) {
+// into their waits. Otherwise every workgroup takes a share. With head
+// attention (na > 0 workgroups at the end run attention and hold its K rows
+// where the others hold gate/up rows) the first NB - na take them, or np
+// exceeds the cap and the launcher does not pick that mode. Returns np.
+__host__ __device__ inline int gu_share(int I, int nkv, int nchmax, int nq, int na, int *gst,
+                                        int *gen) {
   const int cap = GPMAX * NW;
+  if (na > 0) {
+    *gst = 0;
+    *gen = NB - na;
+    return 2 * ((I + 2 * (NB - na) - 1) / (2 * (NB - na)));
+  }
   int a = nkv * nchmax, b = NB - nq;
   int np = b - a > 0 ? 2 * ((I + 2 * (b - a) - 1) / (2 * (b - a))) : cap + 1;
   if (np > cap) {
@@ -521,9 +537,15 @@ __host__ __device__ inline int gu_share(int I, int nkv, int nchmax, int nq, int 
 // the launch arguments: the launcher picks the Qwen2.5-1.5B instantiation for
 // that shape, where folding the dimensions frees the scalar registers that
 // the generic build would spill, and the generic one for every other shape.
-// KB: the KV cache holds bf16 (else f32). MS: more than 16 attention chunks
-// per head (max_seq > 512), each head's merge split over four workgroups.
-template <int kH, int kI, int kV, int kNQ, int kNKV, int kD, bool KB, bool MS>
+// KB: the KV cache holds bf16 (else f32). AM, the attention mode: 0 work
+// items (kv head, 32-position chunk) merged per q head on one workgroup; 1
+// the same with more than 16 chunks per head (max_seq > 512), each head's
+// merge split over four workgroups; 2 head attention (head dim 128, at most
+// 256 positions): 2 nq workgroups at the end of the grid each own a q head
+// and one half of its value columns, hold the head's cached K rows in
+// registers and its value half in LDS (loaded a layer ahead), and publish
+// their share of the attention output with no merge step.
+template <int kH, int kI, int kV, int kNQ, int kNKV, int kD, bool KB, int AM>
 __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
   extern __shared__ float4 sm4[];
   float *xs = (float *)sm4;     // [MAXH] activation for the current phase
@@ -547,13 +569,21 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
   const int qdim = nq * d, kvdim = nkv * d, qkv_rows = qdim + 2 * kvdim;
   const uint32_t TPS = (uint32_t)a.L * kTPL + 2;
   const int nchmax = (a.max_seq + AC - 1) / AC;
+  // head attention: workgroups [NBW, NB) run attention, the others own the
+  // QKV, residual (o, down) and gate/up rows
+  constexpr bool HA = AM == 2;
+  const int NA = HA ? 2 * nq : 0, NBW = NB - NA;
+  const bool is_att = HA && wg >= NBW;
+  const int ah = HA ? max(wg - NBW, 0) >> 1 : 0;  // q head
+  const int avh = HA ? max(wg - NBW, 0) & 1 : 0;  // value half
+  const int ag = ah / gq;                          // its kv head
   // ownership
-  const int qper = (((qkv_rows + NB - 1) / NB) + 1) & ~1;
-  const int q0 = wg * qper, q1 = min(q0 + qper, qkv_rows);
-  const int xper = (H + NB - 1) / NB;
-  const int x0 = wg * xper, x1 = min(x0 + xper, H);
+  const int qper = (((qkv_rows + NBW - 1) / NBW) + 1) & ~1;
+  const int q0 = wg < NBW ? wg * qper : qkv_rows, q1 = min(q0 + qper, qkv_rows);
+  const int xper = (H + NBW - 1) / NBW;
+  const int x0 = wg < NBW ? min(wg * xper, H) : H, x1 = min(x0 + xper, H);
   int gst, gen;
-  const int np = gu_share(I, nkv, nchmax, nq, &gst, &gen);
+  const int np = gu_share(I, nkv, nchmax, nq, NA, &gst, &gen);
   const int gper = 2 * np;  // gate/up rows
   const int g0 = wg >= gst && wg < gen ? (wg - gst) * gper : 2 * I;
   const int g1 = min(g0 + gper, 2 * I);
@@ -618,6 +648,61 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
   auto issue_wdp = [&](int l, int part) {
     if (kv > 0) dma_block(uni(lay[l].wdp), H, j0, kv, wave * cw, cw, wp_s, lane, part);
   };
+
+  // ---- head attention (HA): K rows in the gate/up slot registers, value half
+  // in LDS where the others hold their down block -----------------------------
+  // Thread (r = tid / 8, j8 = tid % 8) holds columns [16 j8, 16 j8 + 16) of
+  // cached positions r + 64 i, i < 4: f32 in kreg(4 i + c), c < 4, or bf16 in
+  // kreg(2 i + c), c < 2.
+  auto kreg = [&](int i) -> u32x4 & { return gu[i / (2 * HC)][(i / HC) & 1][i % HC]; };
+  constexpr int HAD = 128, HAP = 256;                  // head dim, positions
+  constexpr int hvb = HAD / 2 * (KB ? 2 : 4);          // bytes of a value half row
+  // value half rows in LDS as 16-byte chunks, chunk c of row t at slot
+  // t * hvc + (c ^ (t % hvc)): the V sum reads one chunk column of 64
+  // consecutive rows at once, and the swizzle spreads them over the banks
+  constexpr int hvc = hvb / 16;                        // chunks per row
+  uint8_t *hv_s = wdl;                                 // [HAP][HAD / 2] value half
+  float *hq_s = (float *)(wdl + HAP * hvb);            // [HAD] q head
+  float *hk_s = hq_s + HAD;                            // [HAD] this step's k row
+  float *hp_s = hk_s + HAD;                            // [HAP] scaled scores
+  float *ho_s = hp_s + HAP;                            // [HAD / 2] this workgroup's output
+  auto att_kv_rsrc = [&](const float *base, int l) {
+    constexpr int kvb = KB ? 2 : 4;
+    return __builtin_amdgcn_make_buffer_rsrc((void *)((const uint8_t *)base + (size_t)l * a.layer_kv * kvb),
+                                             (short)0, (int)(a.layer_kv * kvb), 0x00020000);
+  };
+  // cached K rows [0, npos) of layer l into kreg; a row past npos reads at
+  // an offset past the buffer (zeros, no traffic), so every load is issued
+  auto att_load_k = [&](int l, int npos) {
+    if (!HA) return;
+    constexpr int kvb = KB ? 2 : 4, nc = KB ? 2 : 4;
+    const __amdgpu_buffer_rsrc_t rk = att_kv_rsrc(a.kc, l);
+    const int r = tid >> 3, j8 = tid & 7;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int t = r + 64 * i;
+      const uint32_t off = t < npos ? (uint32_t)(((ag * a.max_seq + t) * HAD + 16 * j8) * kvb) : 0x80000000u;
+#pragma unroll
+      for (int c = 0; c < nc; c++) kreg(nc * i + c) = __builtin_amdgcn_raw_buffer_load_b128(rk, off, 16 * c, 16);
+    }
+  };
+  // cached value-half rows [0, npos) of layer l into hv_s with direct (DMA)
+  // loads, 1 KB per wave instruction: lane l fills slot 64 i + l, so it
+  // fetches the chunk the swizzle puts there
+  auto att_load_v = [&](int l, int npos) {
+    if (!HA) return;
+    constexpr int kvb = KB ? 2 : 4, rpl = 1024 / hvb;  // rows per load
+    const __amdgpu_buffer_rsrc_t rv = att_kv_rsrc(a.vc, l);
+    const int nld = (npos + rpl - 1) / rpl;
+    for (int i = wave; i < nld; i += NW) {
+      const int t = i * rpl + lane / hvc, c = (lane % hvc) ^ (t % hvc);
+      const uint32_t off = t < npos ? (uint32_t)((((ag * a.max_seq + t) * HAD) + avh * (HAD / 2)) * kvb + c * 16)
+                                    : 0x80000000u;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rv, (__attribute__((address_space(3))) void *)(hv_s + i * 1024), 16, off, 0, 0, 16);
+    }
+  };
+
   // what layer l needs loaded before its first wait
   auto issue_first = [&](int l) {
     issue_wdp(l, 0);
@@ -625,6 +710,256 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
     issue_o(l, true);
     issue_gu(l, true, 0);
   };
+
+  // ---- final norm + head + argmax partial of step s (tag tstep + kTPL L);
+  // `next` issues the next step's first loads once the head's tiles are out
+  auto head_phase = [&](uint32_t s, uint32_t tstep, auto next) {
+    const uint32_t TH = tstep + (uint32_t)a.L * kTPL;
+    float bv = -INFINITY;
+    uint32_t bi = 0xffffffffu;
+    {
+      XPairs<HC> xp;
+      {
+        u32x4 gw[HC];
+        load_gw<HC>(gw, a.final_norm, H, lane);
+        tgather_lin<3>(a.txd, H, TH - kTPL + P_XD, xs, a, &fail_s);
+        mark(a, s, 1 + 5 * a.L);
+        float4 xr[HC][2];
+        norm_x<HC>(xr, xp, xs, gw, H, a.eps, lane);
+        if (wg == 0 && wave == 0) {
+#pragma unroll
+          for (int i = 0; i < HC; i++) {
+            const int c = lane + i * 64;
+            if (c < (H >> 3)) {
+              *(float4 *)(a.normed + c * 8) = xr[i][0];
+              *(float4 *)(a.normed + c * 8 + 4) = xr[i][1];
+            }
+          }
+        }
+      }
+      // this wave's rows v0 + wave*HT + k*NW*HT, two tiles in flight
+      u32x4 ta[HT][HC], tb[HT][HC];
+      const int stride = NW * HT;
+      int r0 = v0 + wave * HT;
+#pragma unroll
+      for (int r = 0; r < HT; r++) ldrow_all<HC>(ta[r], a.head, H, r0 + r, v1 - 1, lane);
+      for (; r0 < v1; r0 += 2 * stride) {
+        const int r1 = r0 + stride;
+#pragma unroll
+        for (int r = 0; r < HT; r++) ldrow_all<HC>(tb[r], a.head, H, r1 + r, v1 - 1, lane);
+#pragma unroll
+        for (int r = 0; r < HT; r++)
+          if (r0 + r < v1) {
+            const float y = dotrow_p<HC>(ta[r], xp);
+            if (lane == 0) a.logits[r0 + r] = y;
+            if (beats(y, (uint32_t)(r0 + r), bv, bi)) {
+              bv = y;
+              bi = (uint32_t)(r0 + r);
+            }
+          }
+        const int r2 = r1 + stride;
+#pragma unroll
+        for (int r = 0; r < HT; r++) ldrow_all<HC>(ta[r], a.head, H, r2 + r, v1 - 1, lane);
+#pragma unroll
+        for (int r = 0; r < HT; r++)
+          if (r1 + r < v1) {
+            const float y = dotrow_p<HC>(tb[r], xp);
+            if (lane == 0) a.logits[r1 + r] = y;
+            if (beats(y, (uint32_t)(r1 + r), bv, bi)) {
+              bv = y;
+              bi = (uint32_t)(r1 + r);
+            }
+          }
+      }
+    }
+    if (s + 1 < a.steps) next();
+    if (lane == 0) best_s[wave] = make_float2(bv, __uint_as_float(bi));
+    __syncthreads();
+    if (tid == 0) {
+      float2 b = best_s[0];
+      for (int w = 1; w < NW; w++)
+        if (beats(best_s[w].x, __float_as_uint(best_s[w].y), b.x, __float_as_uint(b.y)))
+          b = best_s[w];
+      tput(a.targ + 2 * wg, b.x, TH);
+      tput(a.targ + 2 * wg + 1, b.y, TH);
+      mark(a, s, 2 + 5 * a.L);
+    }
+    __syncthreads();
+  };
+
+  // ---- the head-attention workgroups' own loop: per layer, wait for the
+  // head's q and this step's k / value half, attend over every position,
+  // publish, then load the next layer's cached rows; per step, a share of the
+  // head. Their registers hold K, so they run apart from the loop below. --
+  if (HA && is_att) {
+    att_load_k(0, (int)a.pos0);
+    att_load_v(0, (int)a.pos0);
+    for (uint32_t s = 0; s < a.steps; s++) {
+      const uint32_t pos = a.pos0 + s;
+      const int seq = (int)pos + 1;
+      const uint32_t tstep = a.tag_base + s * TPS;
+      for (int l = 0; l < a.L; l++) {
+        tid = opaque(tid);
+        lane = tid & 63;
+        const uint32_t T = tstep + (uint32_t)l * kTPL;
+        // ---- head attention (tag T + P_ATT): q head ah, value columns
+        // [64 avh, 64 avh + 64) of kv head ag, all positions at once ----------
+        // Every wave's direct-to-LDS loads of this layer's value rows have
+        // landed before any wave writes this step's row: a load for a row
+        // past the cached ones (out of range, it writes zeros) could land on
+        // it otherwise. They were issued a layer ago, so this costs no wait.
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+        __syncthreads();
+        // q of the head, this step's k and value half: one tagged word a thread
+        constexpr int nw = 2 * HAD + HAD / 2;
+        if (tid < nw) {
+          const uint64_t *src = tid < HAD       ? a.tq + ah * HAD + tid
+                                : tid < 2 * HAD ? a.tkv + ag * HAD + (tid - HAD)
+                                                : a.tkv + kvdim + ag * HAD + avh * (HAD / 2) + (tid - 2 * HAD);
+          uint64_t w = 0;
+          for (unsigned spins = 0; fail_s == 0; spins++) {
+            w = tload(src);
+            if ((uint32_t)(w >> 32) == T + P_QKV) break;
+            if (spin_fail(a, spins)) {
+              fail_s = 1;
+              break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+          }
+          const float v = __uint_as_float((uint32_t)w);
+          const uint32_t vb = pack_bf16(v, 0.f);  // this step's k and v as its cache slot holds them
+          if (tid < HAD) hq_s[tid] = v;
+          else if (tid < 2 * HAD) hk_s[tid - HAD] = KB ? bf_lo(vb) : v;
+          else {
+            constexpr int per = 16 / (KB ? 2 : 4);  // values per chunk
+            const int j = tid - 2 * HAD, c = j / per;
+            uint8_t *dst = hv_s + (pos * hvc + (c ^ (pos % hvc))) * 16;
+            if (KB) ((uint16_t *)dst)[j % per] = (uint16_t)vb;
+            else ((float *)dst)[j % per] = v;
+          }
+        }
+        __syncthreads();
+        // scores: 16-column partial dots of positions r + 64 i, summed over
+        // the 8 lanes of a position
+        {
+          const int r = tid >> 3, j8 = tid & 7;
+          float4 q4[4], c4[4];
+#pragma unroll
+          for (int c = 0; c < 4; c++) {
+            q4[c] = *(const float4 *)(hq_s + 16 * j8 + 4 * c);
+            c4[c] = *(const float4 *)(hk_s + 16 * j8 + 4 * c);
+          }
+          float sc[4];
+#pragma unroll
+          for (int i = 0; i < 4; i++) {
+            const int t = r + 64 * i;
+            const bool cur = t == (int)pos;
+            float kf[16];
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+              if (KB) {
+                const u32x4 kw = kreg(2 * i + (c >> 1));
+                const uint32_t w0 = (c & 1) ? kw.z : kw.x, w1 = (c & 1) ? kw.w : kw.y;
+                kf[4 * c] = bf_lo(w0);
+                kf[4 * c + 1] = bf_hi(w0);
+                kf[4 * c + 2] = bf_lo(w1);
+                kf[4 * c + 3] = bf_hi(w1);
+              } else {
+                const u32x4 kw = kreg(4 * i + c);
+                kf[4 * c] = __uint_as_float(kw.x);
+                kf[4 * c + 1] = __uint_as_float(kw.y);
+                kf[4 * c + 2] = __uint_as_float(kw.z);
+                kf[4 * c + 3] = __uint_as_float(kw.w);
+              }
+            }
+            float v = 0.f;
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+              const float4 q = q4[c], k = cur ? c4[c] : make_float4(kf[4 * c], kf[4 * c + 1],
+                                                                    kf[4 * c + 2], kf[4 * c + 3]);
+              v = fmaf(q.x, k.x, v);
+              v = fmaf(q.y, k.y, v);
+              v = fmaf(q.z, k.z, v);
+              v = fmaf(q.w, k.w, v);
+            }
+            sc[i] = v;
+          }
+          seg_sum_n<4>(sc, 8);
+          const float scale = 1.0f / sqrtf((float)HAD);
+          if (j8 == 0) {
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+              if (r + 64 * i < seq) hp_s[r + 64 * i] = sc[i] * scale;
+          }
+        }
+        __syncthreads();
+        // softmax over the positions in every wave: lane l holds positions
+        // l + 64 i, the rows whose values it multiplies in the V sum. Wave w
+        // sums columns [8 w, 8 w + 8) of the value half over every position
+        // into LDS, and wave 0 publishes the 64 columns with one store (eight
+        // single-lane stores per wave to one line serialise in the memory
+        // pipeline, and the next layer's loads queue behind them).
+        {
+          float ev[4], mloc = -INFINITY;
+#pragma unroll
+          for (int i = 0; i < 4; i++) {
+            const int t = lane + 64 * i;
+            ev[i] = t < seq ? hp_s[t] : -INFINITY;
+            mloc = fmaxf(mloc, ev[i]);
+          }
+          const float mx = wave_max(mloc);
+          float lsum = 0.f;
+#pragma unroll
+          for (int i = 0; i < 4; i++) {
+            ev[i] = lane + 64 * i < seq ? expf(ev[i] - mx) : 0.f;
+            lsum += ev[i];
+          }
+          const float inv = 1.0f / wave_sum(lsum);
+          float acc[8];
+#pragma unroll
+          for (int j = 0; j < 8; j++) acc[j] = 0.f;
+#pragma unroll
+          for (int i = 0; i < 4; i++) {
+            const int t = lane + 64 * i;
+            const bool in = t < seq;  // rows past seq hold stale LDS: masked, not just weighted by 0
+            float v[8];
+            if (KB) {
+              const u32x4 w = *(const u32x4 *)(hv_s + (t * hvc + (wave ^ (t % hvc))) * 16);
+              v[0] = bf_lo(w.x), v[1] = bf_hi(w.x), v[2] = bf_lo(w.y), v[3] = bf_hi(w.y);
+              v[4] = bf_lo(w.z), v[5] = bf_hi(w.z), v[6] = bf_lo(w.w), v[7] = bf_hi(w.w);
+            } else {
+              const float4 w0 = *(const float4 *)(hv_s + (t * hvc + ((2 * wave) ^ (t % hvc))) * 16);
+              const float4 w1 = *(const float4 *)(hv_s + (t * hvc + ((2 * wave + 1) ^ (t % hvc))) * 16);
+              v[0] = w0.x, v[1] = w0.y, v[2] = w0.z, v[3] = w0.w;
+              v[4] = w1.x, v[5] = w1.y, v[6] = w1.z, v[7] = w1.w;
+            }
+#pragma unroll
+            for (int j = 0; j < 8; j++) acc[j] = fmaf(ev[i], in ? v[j] : 0.f, acc[j]);
+          }
+          wave_sum_n<8>(acc);
+          if (lane == 63) {
+#pragma unroll
+            for (int j = 0; j < 8; j++) ho_s[8 * wave + j] = acc[j] * inv;
+          }
+        }
+        // (every wave has also read the value rows before the next layer's land)
+        __syncthreads();
+        if (tid < HAD / 2) tput(a.tatt + ah * HAD + avh * (HAD / 2) + tid, ho_s[tid], T + P_ATT);
+        // the next layer's cached rows (this step), or the value half of the
+        // next step's layer 0 (its K rows load after the head, so that no K
+        // register is live across the head's tiles)
+        if (l + 1 < a.L) {
+          att_load_k(l + 1, (int)pos);
+          att_load_v(l + 1, (int)pos);
+        } else if (s + 1 < a.steps) {
+          att_load_v(0, (int)pos + 1);
+        }
+        mark(a, s, 2 + 5 * l);
+      }
+      head_phase(s, tstep, [&] { att_load_k(0, (int)pos + 1); });
+    }
+    return;
+  }
 
   issue_first(0);
   for (uint32_t s = 0; s < a.steps; s++) {
@@ -753,13 +1088,14 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
       issue_wdp(l, 1);
 
       // ---- attention partials for (kv head, chunk) items (tag T + P_PART) ----
+      // (AM 0 and 1; head attention follows below)
       // Thread i = tid + u NT holds columns [4 j4, 4 j4 + 4) of position
       // t = i / dq of the chunk (dq = d / 4 lanes per position), K in
       // registers and V staged in LDS. A score is a dq-lane segmented sum;
       // then wave h takes q head h: softmax over the chunk in its lanes and
       // the V sum with each weight read back from the lane that holds it.
       const int nch = (seq + AC - 1) / AC;
-      for (int it = wg; it < nkv * nch; it += NB) {
+      for (int it = HA ? NB : wg; it < nkv * nch; it += NB) {
         const int g = it % nkv, c = it / nkv;
         const int t0 = c * AC, n = min(AC, seq - t0);
         const bool has_cur = (int)pos < t0 + n;  // this step's row ends the chunk
@@ -830,10 +1166,12 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
         for (int u = 0; u < QW; u++) {
           const int i = tid + u * NT, r = i - nqw;
           const float v = __uint_as_float((uint32_t)w[u]);
+          // this step's k and v as its cache slot holds them
+          const float kvv = KB ? bf_lo(pack_bf16(v, 0.f)) : v;
           if (i < nqw) q_s[i] = v;
           else if (i < nw) {
-            if (r < d) kcur[r] = v;
-            else v_s[nold * d + r - d] = v;
+            if (r < d) kcur[r] = kvv;
+            else v_s[nold * d + r - d] = kvv;
           }
         }
         __syncthreads();
@@ -924,21 +1262,21 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
       issue_gu(l, true, 1);
       issue_gu(l, true, 2);
       issue_gu(l, true, 3);
-      issue_gu(l, true, 4);
+      if (!HA) issue_gu(l, true, 4);
 
       // ---- merge: q head h's chunks -> att[h] (tag T + P_ATT), on the last
       // workgroups (attention items start at the first); one wave combines
       // att = sum_c e^(m_c - M) o_c / sum_c e^(m_c - M) l_c. Launches with
       // more than 16 chunks per head (MS) split a head over four workgroups of
       // d / 4 columns each, so no merge gathers more than about 5 words a thread.
-      constexpr int mp = MS ? 4 : 1;
+      constexpr int mp = AM == 1 ? 4 : 1;
       const int mi = NB - 1 - wg, mh = mi / mp, mq = mi - mh * mp;
-      if (mh < nq) {
+      if (!HA && mh < nq) {
         const int dd = d + 2, dw = d / mp, dpw = dw + 2, j0 = mq * dw;
         float *pc = big;                     // [nch][dw + 2]: columns j0 .. j0 + dw, then m, l
         float *wc = big + nch * dpw;         // [nch] chunk weights
         const int base = mh * nchmax * dd;
-        if (!MS)
+        if (AM != 1)
           tgather<2>(a.tpart, [base](int i) { return base + i; }, nch * dd, T + P_PART, pc, a, &fail_s);
         else
           tgather<2>(
@@ -981,6 +1319,9 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
         }
       }
 
+      // with head attention the attention-output wait comes right after QKV,
+      // so the last gate/up slot waits until after it
+      if (HA) issue_gu(l, true, 4);
       issue_wdp(l, 2);
       // ---- gate/up + SwiGLU + down partials (tag T + P_PD) ----------------------
       load_gw<HC>(gw, Lln2, H, lane);
@@ -1089,78 +1430,7 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
 
     }
 
-    // ---- final norm + head + argmax partial (tag tstep + 5L) -----------------
-    const uint32_t TH = tstep + (uint32_t)a.L * kTPL;
-    float bv = -INFINITY;
-    uint32_t bi = 0xffffffffu;
-    {
-      XPairs<HC> xp;
-      {
-        u32x4 gw[HC];
-        load_gw<HC>(gw, a.final_norm, H, lane);
-        tgather_lin<3>(a.txd, H, TH - kTPL + P_XD, xs, a, &fail_s);
-        mark(a, s, 1 + 5 * a.L);
-        float4 xr[HC][2];
-        norm_x<HC>(xr, xp, xs, gw, H, a.eps, lane);
-        if (wg == 0 && wave == 0) {
-#pragma unroll
-          for (int i = 0; i < HC; i++) {
-            const int c = lane + i * 64;
-            if (c < (H >> 3)) {
-              *(float4 *)(a.normed + c * 8) = xr[i][0];
-              *(float4 *)(a.normed + c * 8 + 4) = xr[i][1];
-            }
-          }
-        }
-      }
-      // this wave's rows v0 + wave*HT + k*NW*HT, two tiles in flight
-      u32x4 ta[HT][HC], tb[HT][HC];
-      const int stride = NW * HT;
-      int r0 = v0 + wave * HT;
-#pragma unroll
-      for (int r = 0; r < HT; r++) ldrow_all<HC>(ta[r], a.head, H, r0 + r, v1 - 1, lane);
-      for (; r0 < v1; r0 += 2 * stride) {
-        const int r1 = r0 + stride;
-#pragma unroll
-        for (int r = 0; r < HT; r++) ldrow_all<HC>(tb[r], a.head, H, r1 + r, v1 - 1, lane);
-#pragma unroll
-        for (int r = 0; r < HT; r++)
-          if (r0 + r < v1) {
-            const float y = dotrow_p<HC>(ta[r], xp);
-            if (lane == 0) a.logits[r0 + r] = y;
-            if (beats(y, (uint32_t)(r0 + r), bv, bi)) {
-              bv = y;
-              bi = (uint32_t)(r0 + r);
-            }
-          }
-        const int r2 = r1 + stride;
-#pragma unroll
-        for (int r = 0; r < HT; r++) ldrow_all<HC>(ta[r], a.head, H, r2 + r, v1 - 1, lane);
-#pragma unroll
-        for (int r = 0; r < HT; r++)
-          if (r1 + r < v1) {
-            const float y = dotrow_p<HC>(tb[r], xp);
-            if (lane == 0) a.logits[r1 + r] = y;
-            if (beats(y, (uint32_t)(r1 + r), bv, bi)) {
-              bv = y;
-              bi = (uint32_t)(r1 + r);
-            }
-          }
-      }
-    }
-    if (s + 1 < a.steps) issue_first(0);
-    if (lane == 0) best_s[wave] = make_float2(bv, __uint_as_float(bi));
-    __syncthreads();
-    if (tid == 0) {
-      float2 b = best_s[0];
-      for (int w = 1; w < NW; w++)
-        if (beats(best_s[w].x, __float_as_uint(best_s[w].y), b.x, __float_as_uint(b.y)))
-          b = best_s[w];
-      tput(a.targ + 2 * wg, b.x, TH);
-      tput(a.targ + 2 * wg + 1, b.y, TH);
-      mark(a, s, 2 + 5 * a.L);
-    }
-    __syncthreads();
+    head_phase(s, tstep, [&] { issue_first(0); });
   }
 
   // ---- hand the state back to the per-kernel path ---------------------------
@@ -2195,6 +2465,12 @@ int persist_tags_per_step(int layers) { return layers * (int)kTPL + 2; }
 size_t persist_part_words(int nq, int max_seq, int d) {
   return (size_t)nq * ((max_seq + AC - 1) / AC) * (size_t)(d + 2);
 }
+// down partials, [owner][source][rows per owner]: rows per owner are largest
+// when head attention leaves NB - 2 nq workgroups to own them
+size_t persist_pr_words(int H, int nq) {
+  const int own = NB - 2 * nq > 0 ? NB - 2 * nq : NB;
+  return (size_t)NB * NB * (size_t)((H + own - 1) / own);
+}
 
 bool persist_supported(int H, int I, int qdim, int d, int gq) {
   // H % 32: each wave's H / 8 down columns load 4 words a lane
@@ -2215,18 +2491,21 @@ bool persist_supported(int H, int I, int qdim, int d, int gq) {
 // (attention item staging, merge partials, argmax partials, h share), this
 // workgroup's down column pairs and the layer table; sets the down block's
 // offset in `a`
+static bool persist_head_attention(const PersistArgs &a);
+
 static size_t persist_lds(PersistArgs &a) {
   const int gq = a.nq / a.nkv;
   const size_t attn = (size_t)gq * a.d + a.d + (size_t)AC * a.d + (size_t)gq * AC;
   const int nchm = (a.max_seq + AC - 1) / AC;
   const size_t merge = (size_t)nchm * (a.d + 2) + nchm;
   int gst, gen;
-  const int np = gu_share(a.I, a.nkv, nchm, a.nq, &gst, &gen);
+  const bool ha = persist_head_attention(a);
+  const int np = gu_share(a.I, a.nkv, nchm, a.nq, ha ? 2 * a.nq : 0, &gst, &gen);
   size_t big = attn;
   if (merge > big) big = merge;
   if ((size_t)2 * NB > big) big = 2 * NB;
   if ((size_t)np > big) big = np;
-  const size_t xper = (size_t)(a.H + NB - 1) / NB;
+  const size_t xper = (size_t)(a.H + (NB - (ha ? 2 * a.nq : 0)) - 1) / (NB - (ha ? 2 * a.nq : 0));
   if (64 + NB * xper > big) big = 64 + NB * xper;  // h share, then the down partials
   // the h share sits in the 64 floats before the gathered partials (np is at
   // most GPMAX * NW = 40 on every supported shape; larger would not fit)
@@ -2235,6 +2514,25 @@ static size_t persist_lds(PersistArgs &a) {
   a.lds_wd = (int)wd_off;
   return wd_off * sizeof(float) + (size_t)NW * (np / 2) * (a.H / NW) * 4 +
          (size_t)a.L * sizeof(PersistLayer);
+}
+
+// LDS bytes of a head-attention workgroup (value half, q, k, the scores and
+// its output), which it keeps where the others keep their down block
+static size_t head_attention_lds(int kv_bf16) {
+  return (size_t)256 * 64 * (kv_bf16 ? 2 : 4) + (128 + 128 + 256 + 64) * sizeof(float);
+}
+
+// Head attention (AM 2) runs on the Qwen2.5-1.5B instantiation when every
+// position of the launch fits one workgroup's registers and LDS (max_seq <=
+// 256) and the other 232 workgroups can hold the gate/up rows.
+static bool persist_head_attention(const PersistArgs &a) {
+  const bool qwen15 = a.H == 1536 && a.I == 8960 && a.V == 151936 && a.nq == 12 && a.nkv == 2 &&
+                      a.d == 128;
+  if (!qwen15 || a.max_seq > 256) return false;
+  int gst, gen;
+  const int np = gu_share(a.I, a.nkv, 0, a.nq, 2 * a.nq, &gst, &gen);
+  if (np > GPMAX * NW) return false;
+  return (size_t)NW * (np / 2) * (a.H / NW) * 4 >= head_attention_lds(a.kv_bf16);
 }
 
 bool persist_device_ok(const PersistArgs &a) {
@@ -2259,18 +2557,21 @@ hipError_t launch_decode_persistent(const PersistArgs &a, hipStream_t s) {
                       a.d == 128;
   const bool kb = a.kv_bf16 != 0;
   const bool ms = (a.max_seq + AC - 1) / AC > 16;
-  const void *const fns[8] = {
-      (const void *)decode_persistent_kernel<0, 0, 0, 0, 0, 0, false, false>,
-      (const void *)decode_persistent_kernel<0, 0, 0, 0, 0, 0, true, false>,
-      (const void *)decode_persistent_kernel<1536, 8960, 151936, 12, 2, 128, false, false>,
-      (const void *)decode_persistent_kernel<1536, 8960, 151936, 12, 2, 128, true, false>,
-      (const void *)decode_persistent_kernel<0, 0, 0, 0, 0, 0, false, true>,
-      (const void *)decode_persistent_kernel<0, 0, 0, 0, 0, 0, true, true>,
-      (const void *)decode_persistent_kernel<1536, 8960, 151936, 12, 2, 128, false, true>,
-      (const void *)decode_persistent_kernel<1536, 8960, 151936, 12, 2, 128, true, true>};
-  const int which = 4 * ms + 2 * qwen15 + kb;
+  const bool ha = persist_head_attention(a);
+  const void *const fns[10] = {
+      (const void *)decode_persistent_kernel<0, 0, 0, 0, 0, 0, false, 0>,
+      (const void *)decode_persistent_kernel<0, 0, 0, 0, 0, 0, true, 0>,
+      (const void *)decode_persistent_kernel<1536, 8960, 151936, 12, 2, 128, false, 0>,
+      (const void *)decode_persistent_kernel<1536, 8960, 151936, 12, 2, 128, true, 0>,
+      (const void *)decode_persistent_kernel<0, 0, 0, 0, 0, 0, false, 1>,
+      (const void *)decode_persistent_kernel<0, 0, 0, 0, 0, 0, true, 1>,
+      (const void *)decode_persistent_kernel<1536, 8960, 151936, 12, 2, 128, false, 1>,
+      (const void *)decode_persistent_kernel<1536, 8960, 151936, 12, 2, 128, true, 1>,
+      (const void *)decode_persistent_kernel<1536, 8960, 151936, 12, 2, 128, false, 2>,
+      (const void *)decode_persistent_kernel<1536, 8960, 151936, 12, 2, 128, true, 2>};
+  const int which = ha ? 8 + kb : 4 * ms + 2 * qwen15 + kb;
   const void *fn = fns[which];
-  static bool attr_set[8] = {false, false, false, false, false, false, false, false};
+  static bool attr_set[10] = {false, false, false, false, false, false, false, false, false, false};
   if (!attr_set[which]) {
     hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxLds);
     if (e != hipSuccess) return e;
