@@ -2580,6 +2580,35 @@ hipError_t launch_attn_decode(const AttnDecodeArgs &a, hipStream_t s) {
   return hipGetLastError();
 }
 
+// The MFMA GEMM multiplies every weight by the activation's bf16 hi and lo
+// parts. An infinite weight times a zero lo part is NaN where the
+// reference's f32 chain (gemm_bf16.rs:337-378, bit-identical to the per-token
+// GEMV) gives +-inf, so a NaN output is recomputed here as that chain: left
+// to right from +0, each product rounded before it is added. Outputs that
+// are not NaN are left as they are; with finite weights and activations no
+// output is NaN and the pass only reads Y.
+__global__ void gemm_nan_repair_kernel(float *y, const uint16_t *w, const float *x, int batch, int m, int k) {
+  const size_t n = (size_t)batch * m;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+    if (!__builtin_isnan(y[i])) continue;
+    const size_t b = i / m, r = i - b * m;
+    const uint16_t *wr = w + r * k;
+    const float *xb = x + b * k;
+    float acc = 0.f;
+    for (int j = 0; j < k; j++) acc = __fadd_rn(acc, __fmul_rn(bf16f(wr[j]), xb[j]));
+    y[i] = acc;
+  }
+}
+
+hipError_t launch_gemm_nan_repair(float *y, const uint16_t *w, const float *x, int batch, int m, int k,
+                                  hipStream_t s) {
+  const size_t n = (size_t)batch * m;
+  if (!n) return hipSuccess;
+  const size_t blocks = std::min<size_t>(nblk(n, 256), 2048);
+  hipLaunchKernelGGL(gemm_nan_repair_kernel, dim3((unsigned)blocks), dim3(256), 0, s, y, w, x, batch, m, k);
+  return hipGetLastError();
+}
+
 hipError_t launch_fill_zero(float *y, size_t n, hipStream_t s) {
   if (!n) return hipSuccess;
   hipLaunchKernelGGL(fill_zero_kernel, dim3(nblk(n, 256)), dim3(256), 0, s, y, n);

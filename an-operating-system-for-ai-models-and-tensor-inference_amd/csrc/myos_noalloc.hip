@@ -103,6 +103,7 @@ int myos_gemm_bf16_noalloc(float *y, size_t y_len, const uint16_t *w, size_t w_l
     g.ws = ws;
     g.ws_cap = wsf;
     e = launch_gemm(g, EPI_STORE, s);
+    if (e == hipSuccess) e = launch_gemm_nan_repair(y, w, x, (int)batch, (int)m, (int)k, s);
   }
   return e == hipSuccess ? MYOS_OK : MYOS_E_HIP;
 }

@@ -112,6 +112,7 @@ int myos_gemm_bf16(float *y, size_t y_len, const uint16_t *w, size_t w_len, cons
     g.ws = ws;
     g.ws_cap = wsf;
     e = launch_gemm(g, EPI_STORE, s);
+    if (e == hipSuccess) e = launch_gemm_nan_repair(y, w, x, (int)batch, (int)m, (int)k, s);
   }
   hipError_t f1 = hipFreeAsync(hi, s), f2 = hipFreeAsync(lo, s);
   hipError_t f3 = ws ? hipFreeAsync(ws, s) : hipSuccess;

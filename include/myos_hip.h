@@ -83,7 +83,12 @@ int myos_gemm_bf16(float *y, size_t y_len, const uint16_t *w, size_t w_len, cons
  * myos_gemm_bf16_noalloc_max_scratch() bytes (32 MiB) per GPU, held until
  * the process ends. A call needing more (myos_gemm_bf16_noalloc_scratch)
  * returns MYOS_E_SCRATCH before anything is launched. All calls on one GPU
- * share that GPU's array: calls that overlap on one GPU race. */
+ * share that GPU's array: calls that overlap on one GPU race. The first call
+ * on a device resolves the array's address (hipGetSymbolAddress) and sets the
+ * tile kernels' LDS limits, which stream capture does not record: make one
+ * call outside capture on each device before capturing this entry point.
+ * Outputs that come out NaN (an infinite weight times a zero activation
+ * part) are recomputed as the reference's f32 chain, as in myos_gemm_bf16. */
 int myos_gemm_bf16_noalloc(float *y, size_t y_len, const uint16_t *w, size_t w_len,
                            const float *x, size_t x_len, size_t batch, size_t m, size_t k,
                            myos_stream_t stream);
