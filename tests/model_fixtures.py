@@ -149,6 +149,34 @@ def bf16_kv_fixture():
     return fixture_shape(), t
 
 
+def bf16_kv_fixture_wide():
+    """bf16_kv_fixture widened to a shape the cooperative decode kernels take
+    (hidden 64, 2 q heads / 1 kv head of dim 32, intermediate 64, vocab 8,
+    eps 0): token 0 embeds to 64 ones, so its norm is exactly 1 and v starts
+    [1 + 3 * 2^-8, 1 + 2^-9, 0, ...]; q = k = 0; o_proj copies head 0's
+    first two output columns into stream rows 0 and 1; the MLP is zero. The
+    hidden state after the layer is 1 + [v0, v1, 0, ...] with v as the cache
+    holds it, exactly, in any summation order."""
+    s = shape_dict(64, 2, 1, 32, 64, 8, 1, 0.0)
+    t = {name: bits(np.zeros(shp, np.float32)) for name, shp in tensor_shapes(s).items()}
+    emb = np.zeros((8, 64), np.float32)
+    emb[0] = 1.0
+    emb[1, :2] = [2.0, -1.0]
+    t["model.embed_tokens.weight"] = bits(emb)
+    t["model.norm.weight"] = bits(np.ones(64, np.float32))
+    p = "model.layers.0."
+    for n in ("input_layernorm.weight", "post_attention_layernorm.weight"):
+        t[p + n] = bits(np.ones(64, np.float32))
+    wv = np.zeros((32, 64), np.float32)
+    wv[0, :2] = [1.0, 3.0 * 2.0 ** -8]
+    wv[1, :2] = [1.0, 2.0 ** -9]
+    t[p + "self_attn.v_proj.weight"] = bits(wv)
+    wo = np.zeros((64, 64), np.float32)
+    wo[0, 0] = wo[1, 1] = 1.0
+    t[p + "self_attn.o_proj.weight"] = bits(wo)
+    return s, t
+
+
 # ------------------------------------------------------------- rich map ----
 
 _PAT = np.array([0.5, -0.25, 1.0, 0.0, -1.0, 0.125, 2.0, -0.5], np.float32)

@@ -34,7 +34,9 @@ def open_pair(tmp_path, s, t, max_seq, kv=myos.KV_F32, name="m.safetensors", tie
     path = str(tmp_path / name)
     write_safetensors(path, t)
     g = myos.Model.open(path, to_block_shape(s, tied), kv, max_seq)
-    o = oracle.Model(s, t, max_seq, threads=4)
+    # a bf16 cache is compared with the oracle's bf16 mode (K/V rounded to
+    # nearest even when stored, the step's own row too)
+    o = oracle.Model(s, t, max_seq, threads=4, kv_bf16=kv == myos.KV_BF16)
     return g, o
 
 
@@ -238,7 +240,9 @@ def test_random_small_models(tmp_path, kv, dims):
     prompt = rng.integers(0, s["vocab"], 17)
     g.prefill(prompt)
     assert o.prefill(prompt) == 0
-    tol = 1e-4 if kv == myos.KV_F32 else 2e-2
+    # f32 cache: summation order only; bf16 cache: a cache value a few f32
+    # ulps away from the oracle's may round to the neighbouring bf16 value
+    tol = 1e-4 if kv == myos.KV_F32 else 2e-3
     assert max_rel(g.logits(), o.logits()) < tol
     assert max_rel(g.hidden(), o.hidden()) < tol
     # teacher-forced decode: both fed the oracle's greedy id
@@ -248,8 +252,7 @@ def test_random_small_models(tmp_path, kv, dims):
         assert o.forward_token(tok, pos) == 0
         g.forward_token(tok, pos)
         assert max_rel(g.logits(), o.logits()) < tol, step
-        if kv == myos.KV_F32:
-            assert_logits_parity(g.logits(), o.logits(), f"step {step}")
+        assert_logits_parity(g.logits(), o.logits(), f"step {step}")
     g.close()
 
 

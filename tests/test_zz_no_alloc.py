@@ -51,3 +51,35 @@ def test_noalloc_gemm_refuses_past_scratch():
     assert e.value.kind == "Scratch"
     torch.cuda.synchronize()
     assert bool((y == 7.0).all())
+
+
+def test_noalloc_gemm_under_graph_capture():
+    """The entry point recorded into a graph (after one call outside capture
+    has set the device up) and replayed three times, with eager GPU work and
+    synchronisations between replays: every replay equals the eager
+    myos_gemm_bf16 result bit for bit."""
+    import torch
+    batch, m, k = 64, 512, 1536
+    w, x = _inputs(torch, batch, m, k, 3)
+    y_ref = torch.empty((batch, m), device="cuda")
+    myos.gemm_bf16(y_ref, w, x, batch, m, k)
+    y = torch.full((batch, m), float("nan"), device="cuda")
+    myos.gemm_bf16_noalloc(y, w, x, batch, m, k)  # set-up call, outside capture
+    torch.cuda.synchronize()
+    assert torch.equal(y, y_ref)
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            myos.gemm_bf16_noalloc(y, w, x, batch, m, k)
+    torch.cuda.current_stream().wait_stream(side)
+    for rep in range(3):
+        y.fill_(float("nan"))
+        other = torch.randn(256, 256, device="cuda") @ torch.randn(256, 256, device="cuda")
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y, y_ref), rep
+        del other
+
