@@ -75,6 +75,11 @@ EXPORTS = {
     "myos_rope_f32_inplace": ([P, SZ, U32, SZ, F32, P], I32),
     "myos_gqa_attn_f32": ([P, SZ, P, SZ, P, SZ, P, SZ, P, SZ, SZ, SZ, SZ, SZ, I32, SZ, P], I32),
     "myos_swiglu_mul_f32": ([P, SZ, P, SZ, P, SZ, P], I32),
+    "myos_swiglu_bf16": ([P, SZ, P, SZ, P, SZ, P, SZ, P, SZ, P, SZ, P, SZ, P, SZ, SZ, SZ, P], I32),
+    "myos_silu_f32": ([P, SZ, P, SZ, P], I32),
+    "myos_rmsnorm_f32": ([P, SZ, P, SZ, P, SZ, F32, P], I32),
+    "myos_rope_inv_freqs": ([P, SZ, SZ, F32, P], I32),
+    "myos_attn_scale_f32": ([SZ, C.POINTER(F32)], I32),
     "myos_greedy_token": ([P, P, SZ, P], I32),
     "myos_stream_sync": ([P], I32),
     "myos_block_shape_preset": ([I32, C.POINTER(BlockShape)], I32),
@@ -84,6 +89,8 @@ EXPORTS = {
     "myos_forward_token": ([P, U32, SZ], I32),
     "myos_greedy_decode": ([P, SZ, P], I32),
     "myos_cache_len": ([P], SZ),
+    "myos_attention_layer": ([P, SZ, SZ, P, P, SZ], I32),
+    "myos_kv_advance": ([P], I32),
     "myos_max_seq": ([P], SZ),
     "myos_copy_logits": ([P, P, SZ], I32),
     "myos_copy_hidden": ([P, P, SZ], I32),
@@ -274,6 +281,42 @@ def swiglu_mul_f32(h, gate, up, stream=None):
            "swiglu_mul_f32")
 
 
+def swiglu_bf16(y, x, gate_w, up_w, down_w, gate, up, h, hidden, intermediate, stream=None):
+    """swiglu.rs:184-213: y = W_d (silu(W_g x) * (W_u x)); gate/up/h scratch."""
+    args = [_f32(y, "y"), _f32(x, "x"), _w16(gate_w, "gate_w"), _w16(up_w, "up_w"),
+            _w16(down_w, "down_w"), _f32(gate, "gate"), _f32(up, "up"), _f32(h, "h")]
+    flat = [v for pn in args for v in pn]
+    _check(lib().myos_swiglu_bf16(*flat, hidden, intermediate, _stream(stream)), "swiglu_bf16")
+
+
+def silu_f32(y, z, stream=None):
+    """swiglu.rs:113-115, elementwise."""
+    yp, yn = _f32(y, "y")
+    zp, zn = _f32(z, "z")
+    _check(lib().myos_silu_f32(yp, yn, zp, zn, _stream(stream)), "silu_f32")
+
+
+def rmsnorm_f32(y, weight, x, eps, stream=None):
+    """bf16.rs:200-216 (f32 gamma)."""
+    yp, yn = _f32(y, "y")
+    wp, wn = _f32(weight, "weight")
+    xp, xn = _f32(x, "x")
+    _check(lib().myos_rmsnorm_f32(yp, yn, wp, wn, xp, xn, eps, _stream(stream)), "rmsnorm_f32")
+
+
+def rope_inv_freqs(inv_freq, head_dim, theta, stream=None):
+    """rope.rs:89-98 into a device tensor of head_dim / 2 floats."""
+    ip, n = _f32(inv_freq, "inv_freq")
+    _check(lib().myos_rope_inv_freqs(ip, n, head_dim, theta, _stream(stream)), "rope_inv_freqs")
+
+
+def attn_scale_f32(head_dim) -> float:
+    """gqa.rs:158-163."""
+    out = C.c_float()
+    _check(lib().myos_attn_scale_f32(head_dim, C.byref(out)), "attn_scale_f32")
+    return out.value
+
+
 def greedy_token(logits, out=None, stream=None) -> int:
     """model_core/src/lib.rs:157-167; returns the id (syncs the stream)."""
     import torch
@@ -348,6 +391,23 @@ class Model:
         _check(lib().myos_decode_forced(self._h, t.ctypes.data_as(P), t.size,
                                         out.ctypes.data_as(P)), "decode_forced")
         return [int(v) for v in out[:t.size]]
+
+    def attention_layer(self, layer: int, pos: int, residual, proj_in):
+        """attn_wire.rs:207-313 on the model's weights: returns residual +
+        o_proj(attention(proj_in)); stores the layer's K/V row at pos (the
+        cursor does not move: kv_advance)."""
+        import numpy as np
+        r = np.array(residual, dtype=np.float32, copy=True)
+        x = np.ascontiguousarray(proj_in, dtype=np.float32)
+        if r.size != x.size:
+            raise MyosError(E_SHAPE, "attention_layer")
+        _check(lib().myos_attention_layer(self._h, layer, pos, r.ctypes.data_as(P),
+                                          x.ctypes.data_as(P), r.size), "attention_layer")
+        return r
+
+    def kv_advance(self):
+        """KvCache::advance (kv_cache.rs:226-232)."""
+        _check(lib().myos_kv_advance(self._h), "kv_advance")
 
     def debug_raise_wait_error(self):
         """Test hook: the next persistent launch's waits give up at once."""

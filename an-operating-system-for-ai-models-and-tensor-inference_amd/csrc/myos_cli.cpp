@@ -19,7 +19,7 @@
 //                                     defaults to 128 there
 //
 // and, for the device: --model-shape 1.5b|7b, --kv f32|bf16,
-// --decode-path auto|kernels|persistent, --no-graph, and two verification
+// --decode-path auto|kernels|persistent|streamed, --no-graph, and two verification
 // passes run after the timed decode (outside its timing): --gaps re-runs the
 // decode step by step and records every step's top-1 / top-2 logit gap;
 // --teacher-forced (with --ref-ids) feeds the reference ids instead and
@@ -59,7 +59,7 @@ namespace {
 const char *kUsage =
     "myos [--weights PATH] [--block-fixture] [--steps N] [--threads N] [--fingerprint-dir DIR] "
     "[--prompt-ids PATH] [--ref-ids PATH] [--arena-s1] [--warmup N] [--repeats N] "
-    "[--model-shape 1.5b|7b] [--kv f32|bf16] [--decode-path auto|kernels|persistent] "
+    "[--model-shape 1.5b|7b] [--kv f32|bf16] [--decode-path auto|kernels|persistent|streamed] "
     "[--no-graph] [--gaps] [--teacher-forced] [--no-hash]";
 
 constexpr double kHbmPeakGBps = 8000.0;  // MI355X HBM3E
@@ -86,7 +86,7 @@ const char *flag_noun(const std::string &name) {
   if (name == "--warmup") return "a non-negative integer";
   if (name == "--model-shape") return "1.5b or 7b";
   if (name == "--kv") return "f32 or bf16";
-  if (name == "--decode-path") return "auto, kernels or persistent";
+  if (name == "--decode-path") return "auto, kernels, persistent or streamed";
   return "a path";
 }
 
@@ -221,7 +221,8 @@ int parse_cli(int argc, char **argv, Cli &c, std::string &err) {
       if (v == "auto") c.decode = MYOS_DECODE_AUTO;
       else if (v == "kernels") c.decode = MYOS_DECODE_KERNELS;
       else if (v == "persistent") c.decode = MYOS_DECODE_PERSISTENT;
-      else return err = "--decode-path needs auto, kernels or persistent, got `" + v + "`", -1;
+      else if (v == "streamed") c.decode = MYOS_DECODE_STREAMED;
+      else return err = "--decode-path needs auto, kernels, persistent or streamed, got `" + v + "`", -1;
       c.has_decode = true;
       continue;
     }
@@ -538,12 +539,17 @@ int write_text(const std::string &dir, const char *name, const std::string &text
   return f ? 0 : -1;
 }
 
+// the name run_fingerprint.json and metrics.json give a decode path
+const char *decode_path_name(int dp) {
+  return dp == MYOS_DECODE_PERSISTENT ? "persistent" : dp == MYOS_DECODE_STREAMED ? "streamed" : "kernels";
+}
+
 // run_fingerprint.json (fingerprint.rs:161-203) + device fields
 std::string fingerprint_json(const Cli &c, const myos_block_shape &s, bool weights, bool pinned,
                              const Run &r, int argc, char **argv) {
   const char *layout = !weights ? "block-fixture" : pinned ? "qwen25_1_5b" : "not-qwen25-1.5b";
   const std::string model_id = weights && pinned ? json_str("Qwen/Qwen2.5-1.5B-Instruct") : "null";
-  const char *dp = r.decode_path == MYOS_DECODE_PERSISTENT ? "persistent" : "kernels";
+  const char *dp = decode_path_name(r.decode_path);
   std::vector<std::pair<std::string, std::string>> f = {
       {"model_id", model_id},
       {"model_sha256", r.sha256.empty() ? "null" : json_str(r.sha256)},
@@ -658,7 +664,7 @@ std::string metrics_json(const Cli &c, const myos_block_shape &shape, const Run 
       {"device_decode_tok_s", r.dev_decode_ms > 0 ? json_num(n_gen / (r.dev_decode_ms * 1e-3)) : "null"},
       {"device_weight_bytes", std::to_string(r.weight_bytes)},
       {"device_kv_bytes", std::to_string(r.kv_bytes)},
-      {"decode_path", json_str(r.decode_path == MYOS_DECODE_PERSISTENT ? "persistent" : "kernels")},
+      {"decode_path", json_str(decode_path_name(r.decode_path))},
       {"M_hwm_KiB", kib(r.hwm)},
       {"verify_mode", verified ? json_str(r.verify_mode) : "null"},
       {"verify_agree", verified ? std::to_string(agree) : "null"},
@@ -731,7 +737,8 @@ int main(int argc, char **argv) {
     if (c.has_kv) job.device_args.push_back(c.kv == MYOS_KV_BF16 ? "--kv=bf16" : "--kv=f32");
     if (c.has_decode)
       job.device_args.push_back(c.decode == MYOS_DECODE_PERSISTENT ? "--decode-path=persistent"
-                                : c.decode == MYOS_DECODE_KERNELS ? "--decode-path=kernels"
+                                : c.decode == MYOS_DECODE_KERNELS  ? "--decode-path=kernels"
+                                : c.decode == MYOS_DECODE_STREAMED ? "--decode-path=streamed"
                                                                    : "--decode-path=auto");
     if (c.no_graph) job.device_args.push_back("--no-graph");
     job.device_args.push_back("--no-hash");
@@ -773,17 +780,13 @@ int main(int argc, char **argv) {
     }
   }
   r.tokens.assign(c.steps, 0);
-  // the weights file is hashed on a thread while the run goes on
-  std::string sha;
-  std::thread hasher;
-  if (weights && !c.no_hash)
-    hasher = std::thread([&sha, path] {
-      char hex[65];
-      if (myos_sha256_file(path.c_str(), hex) == MYOS_OK) sha = hex;
-    });
   const int rc = decode_timed(path, shape, c, c.has_ref ? &ref : nullptr, r);
-  if (hasher.joinable()) hasher.join();
-  r.sha256 = sha;
+  // the weights file is hashed after the run, so that reading it takes no
+  // disk or CPU from the load, prefill or decode being timed
+  if (rc == 0 && weights && !c.no_hash) {
+    char hex[65];
+    if (myos_sha256_file(path.c_str(), hex) == MYOS_OK) r.sha256 = hex;
+  }
   if (c.block_fixture) unlink(tmpl);
   if (rc) {
     if (c.block_fixture)

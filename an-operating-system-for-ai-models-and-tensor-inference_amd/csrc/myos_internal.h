@@ -71,6 +71,9 @@ hipError_t launch_gqa_general(float *y, const float *q, const float *k, const fl
                               float *probs, float *scratch, int nq, int nkv, int d, int seq,
                               int mask, size_t query_pos, hipStream_t s);
 hipError_t launch_swiglu_mul(float *h, const float *g, const float *u, size_t n, hipStream_t s);
+hipError_t launch_rmsnorm_f32(float *y, const float *g, const float *x, size_t n, float eps,
+                              hipStream_t s);
+hipError_t launch_silu(float *y, const float *z, size_t n, hipStream_t s);
 int argmax_parts(size_t n);
 hipError_t launch_argmax_partial(const float *logits, size_t n, float2 *part, hipStream_t s);
 

@@ -826,14 +826,19 @@ __global__ void embed_gather_kernel(float *out, const uint16_t *table, size_t hi
     out[j] = bf16f(row[j]);
 }
 
+__device__ __forceinline__ float gain(const uint16_t *g, size_t j) { return bf16f(g[j]); }
+__device__ __forceinline__ float gain(const float *g, size_t j) { return g[j]; }
+
+// rmsnorm_bf16_weight (bf16 gains) and rmsnorm_f32 (f32 gains)
+template <class G>
 __global__ void __launch_bounds__(kBlock)
-    rmsnorm_kernel(float *y, const uint16_t *g, const float *x, size_t n, float eps) {
+    rmsnorm_kernel(float *y, const G *g, const float *x, size_t n, float eps) {
   __shared__ float red4[4];
   float ss = 0.f;
   for (size_t j = threadIdx.x; j < n; j += kBlock) ss += x[j] * x[j];
   const float tot = block_sum(ss, red4);
   const float inv = 1.0f / sqrtf(tot / (float)n + eps);
-  for (size_t j = threadIdx.x; j < n; j += kBlock) y[j] = bf16f(g[j]) * (x[j] * inv);
+  for (size_t j = threadIdx.x; j < n; j += kBlock) y[j] = gain(g, j) * (x[j] * inv);
 }
 
 // cs[p] = (cos, sin) of pair p, evaluated on the host (rope.rs:186-193)
@@ -902,6 +907,11 @@ __global__ void __launch_bounds__(kBlock)
 __global__ void swiglu_mul_kernel(float *h, const float *g, const float *u, size_t n) {
   size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
   if (i < n) h[i] = silu(g[i]) * u[i];
+}
+
+__global__ void silu_kernel(float *y, const float *z, size_t n) {
+  size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
+  if (i < n) y[i] = silu(z[i]);
 }
 
 constexpr int kArgmaxPerBlock = 4096;
@@ -2535,6 +2545,7 @@ hipError_t launch_gemv(const GemvArgs &a, GemvX xm, GemvEpi epi, hipStream_t s, 
   if (xm == X_PLAIN && epi == EPI_STORE) return pick_gemv<X_PLAIN, EPI_STORE>(a, s, nparts);
   if (xm == X_PLAIN && epi == EPI_RESID) return pick_gemv<X_PLAIN, EPI_RESID>(a, s, nparts);
   if (xm == X_NORM && epi == EPI_QKV) return pick_gemv<X_NORM, EPI_QKV>(a, s, nparts);
+  if (xm == X_PLAIN && epi == EPI_QKV) return pick_gemv<X_PLAIN, EPI_QKV>(a, s, nparts);
   if (xm == X_NORM && epi == EPI_GU) return pick_gemv<X_NORM, EPI_GU>(a, s, nparts);
   if (xm == X_NORM && epi == EPI_HEAD) return pick_gemv<X_NORM, EPI_HEAD>(a, s, nparts);
   return hipErrorInvalidValue;
@@ -2630,7 +2641,7 @@ hipError_t launch_embed_gather(float *out, const uint16_t *table, size_t hidden,
 
 hipError_t launch_rmsnorm(float *y, const uint16_t *g, const float *x, size_t n, float eps,
                           hipStream_t s) {
-  hipLaunchKernelGGL(rmsnorm_kernel, dim3(1), dim3(kBlock), 0, s, y, g, x, n, eps);
+  hipLaunchKernelGGL(rmsnorm_kernel<uint16_t>, dim3(1), dim3(kBlock), 0, s, y, g, x, n, eps);
   return hipGetLastError();
 }
 
@@ -2646,6 +2657,18 @@ hipError_t launch_gqa_general(float *y, const float *q, const float *k, const fl
                               int mask, size_t query_pos, hipStream_t s) {
   hipLaunchKernelGGL(gqa_general_kernel, dim3(nq), dim3(kBlock), 0, s, y, q, k, v, probs,
                      scratch, nq, nkv, d, seq, mask, (unsigned long long)query_pos);
+  return hipGetLastError();
+}
+
+hipError_t launch_rmsnorm_f32(float *y, const float *g, const float *x, size_t n, float eps,
+                              hipStream_t s) {
+  hipLaunchKernelGGL(rmsnorm_kernel<float>, dim3(1), dim3(kBlock), 0, s, y, g, x, n, eps);
+  return hipGetLastError();
+}
+
+hipError_t launch_silu(float *y, const float *z, size_t n, hipStream_t s) {
+  if (!n) return hipSuccess;
+  hipLaunchKernelGGL(silu_kernel, dim3(nblk(n, 256)), dim3(256), 0, s, y, z, n);
   return hipGetLastError();
 }
 

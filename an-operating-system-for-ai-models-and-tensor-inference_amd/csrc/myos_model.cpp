@@ -1055,6 +1055,60 @@ int myos_decode_forced(myos_model *m, const uint32_t *ids, size_t steps, uint32_
 
 size_t myos_cache_len(const myos_model *m) { return m ? m->len : 0; }
 
+// attention_layer, attn_wire.rs:207-313: residual += o_proj(attention(q, k, v
+// of proj_in)) for one layer at position pos = the cache cursor, storing the
+// layer's K/V row at pos; the cursor does not move (myos_kv_advance moves
+// it). residual and proj_in are host vectors of `hidden` floats. Every check
+// runs before anything is launched, so on an error residual and the cache
+// are unchanged.
+int myos_attention_layer(myos_model *m, size_t layer, size_t pos, float *residual, const float *proj_in,
+                         size_t len) {
+  if (!m || !residual || !proj_in) return MYOS_E_ARG;
+  if (m->poisoned) return MYOS_E_HIP;
+  if (len != m->s.hidden) return MYOS_E_SHAPE;
+  if (layer >= m->s.num_layers) return MYOS_E_KV_RANGE;
+  if (pos != m->len) return MYOS_E_POSITION;
+  if (pos >= m->max_seq) return MYOS_E_KV_FULL;
+  const myos_block_shape &s = m->s;
+  const DevLayer &L = m->layers[layer];
+  int rc = write_state(m, (uint32_t)pos, 0, 0, 1);
+  if (rc) return rc;
+  HIP_TRY(hipMemcpyAsync(m->x, residual, len * sizeof(float), hipMemcpyHostToDevice, m->stream));
+  HIP_TRY(hipMemcpyAsync(m->normed, proj_in, len * sizeof(float), hipMemcpyHostToDevice, m->stream));
+  // q/k/v GEMV of the caller's vector (no norm prologue) + bias, RoPE, K/V store
+  GemvArgs g;
+  g.w = L.wqkv;
+  g.x = m->normed;
+  g.m = (int)m->qkv_rows;
+  g.k = (int)s.hidden;
+  g.bias = L.bqkv;
+  g.rope = m->rope;
+  g.pos_ptr = m->state;
+  g.q_out = m->q;
+  g.kc = m->kc_layer(layer);
+  g.vc = m->vc_layer(layer);
+  g.kv_bf16 = m->kv_bf16;
+  g.max_seq = (int)m->max_seq;
+  g.q_dim = (int)m->q_dim;
+  g.kv_dim = (int)m->kv_dim;
+  g.head_dim = (int)s.head_dim;
+  HIP_TRY(launch_gemv(g, X_PLAIN, EPI_QKV, m->stream));
+  rc = enq_kernel(m, MYOS_K_ATTN, layer, false);
+  if (!rc) rc = enq_kernel(m, MYOS_K_O, layer, false);
+  if (rc) return rc;
+  HIP_TRY(hipMemcpyAsync(residual, m->x, len * sizeof(float), hipMemcpyDeviceToHost, m->stream));
+  HIP_TRY(hipStreamSynchronize(m->stream));
+  return MYOS_OK;
+}
+
+// KvCache::advance, kv_cache.rs:226-232: one step of the shared cursor
+int myos_kv_advance(myos_model *m) {
+  if (!m) return MYOS_E_ARG;
+  if (m->len >= m->max_seq) return MYOS_E_KV_FULL;
+  m->len += 1;
+  return write_state(m, (uint32_t)m->len, 0, 0, 0);
+}
+
 int myos_cache_clear(myos_model *m) {
   if (!m) return MYOS_E_ARG;
   m->len = 0;

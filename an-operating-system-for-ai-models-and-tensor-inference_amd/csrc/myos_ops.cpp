@@ -214,6 +214,83 @@ int myos_swiglu_mul_f32(float *h, size_t h_len, const float *gate, size_t gate_l
   return hip_status(launch_swiglu_mul(h, gate, up, gate_len, S(stream)));
 }
 
+// swiglu.rs:184-213: gate = W_g x, up = W_u x, h = silu(gate) * up, y = W_d h
+// (the three GEMVs and the product on the device; every check first, so on
+// an error y, gate, up and h are unchanged)
+int myos_swiglu_bf16(float *y, size_t y_len, const float *x, size_t x_len, const uint16_t *gate_w,
+                     size_t gate_w_len, const uint16_t *up_w, size_t up_w_len, const uint16_t *down_w,
+                     size_t down_w_len, float *gate, size_t gate_len, float *up, size_t up_len,
+                     float *h, size_t h_len, size_t hidden, size_t intermediate,
+                     myos_stream_t stream) {
+  if (hidden == 0 || intermediate == 0) return MYOS_E_SHAPE;
+  if (y_len != hidden || x_len != hidden) return MYOS_E_SHAPE;
+  if (gate_len != intermediate || up_len != intermediate || h_len != intermediate) return MYOS_E_SHAPE;
+  size_t wn;
+  if (!mul_ok(hidden, intermediate, &wn)) return MYOS_E_SHAPE;
+  if (gate_w_len != wn || up_w_len != wn || down_w_len != wn) return MYOS_E_SHAPE;
+  if (hidden > INT32_MAX || intermediate > INT32_MAX) return MYOS_E_SHAPE;
+  hipStream_t s = S(stream);
+  GemvArgs a;
+  a.x = x;
+  a.k = (int)hidden;
+  a.m = (int)intermediate;
+  a.w = gate_w;
+  a.y = gate;
+  hipError_t e = launch_gemv(a, X_PLAIN, EPI_STORE, s);
+  if (e == hipSuccess) {
+    a.w = up_w;
+    a.y = up;
+    e = launch_gemv(a, X_PLAIN, EPI_STORE, s);
+  }
+  if (e == hipSuccess) e = launch_swiglu_mul(h, gate, up, intermediate, s);
+  if (e == hipSuccess) {
+    GemvArgs d;
+    d.w = down_w;
+    d.x = h;
+    d.m = (int)hidden;
+    d.k = (int)intermediate;
+    d.y = y;
+    e = launch_gemv(d, X_PLAIN, EPI_STORE, s);
+  }
+  return hip_status(e);
+}
+
+// swiglu.rs:113-115, elementwise: y[i] = z[i] / (1 + expf(-z[i]))
+int myos_silu_f32(float *y, size_t y_len, const float *z, size_t z_len, myos_stream_t stream) {
+  if (y_len != z_len) return MYOS_E_SHAPE;
+  return hip_status(launch_silu(y, z, z_len, S(stream)));
+}
+
+// bf16.rs:200-216: rmsnorm_bf16_weight with an f32 gamma
+int myos_rmsnorm_f32(float *y, size_t y_len, const float *weight, size_t weight_len, const float *x,
+                     size_t x_len, float eps, myos_stream_t stream) {
+  if (x_len == 0 || y_len != x_len || weight_len != x_len) return MYOS_E_SHAPE;
+  return hip_status(launch_rmsnorm_f32(y, weight, x, x_len, eps, S(stream)));
+}
+
+// rope.rs:89-98: inv_freq[i] = 1 / powf(theta, f32(2 i) / f32(head_dim)),
+// evaluated with the reference's expression and libm call (as the decode
+// kernels' cos/sin tables are) and copied to the device
+int myos_rope_inv_freqs(float *inv_freq, size_t len, size_t head_dim, float theta,
+                        myos_stream_t stream) {
+  if (head_dim == 0 || head_dim % 2 != 0 || len != head_dim / 2) return MYOS_E_SHAPE;
+  std::vector<float> t(len);
+  for (size_t i = 0; i < len; i++) t[i] = 1.0f / powf(theta, (float)(2 * i) / (float)head_dim);
+  hipStream_t s = S(stream);
+  hipError_t e = hipMemcpyAsync(inv_freq, t.data(), len * sizeof(float), hipMemcpyHostToDevice, s);
+  if (e == hipSuccess) e = hipStreamSynchronize(s);  // the host table must outlive the copy
+  return hip_status(e);
+}
+
+// gqa.rs:158-163: 1 / sqrtf(head_dim), the scale every attention kernel
+// here multiplies a finished dot by
+int myos_attn_scale_f32(size_t head_dim, float *out) {
+  if (!out) return MYOS_E_ARG;
+  if (head_dim == 0) return MYOS_E_SHAPE;
+  *out = 1.0f / sqrtf((float)head_dim);
+  return MYOS_OK;
+}
+
 // model_core/src/lib.rs:157-167
 int myos_greedy_token(uint32_t *out, const float *logits, size_t n, myos_stream_t stream) {
   if (!out) return MYOS_E_ARG;

@@ -190,6 +190,15 @@ def run_arena(path, shape_name, prompt, ref_ids, n_steps, kv, warmup, repeats):
             "exit": r.returncode, "run_dir": os.path.join(d, "run")}
 
 
+def workload_name(is7b, n_prompt, n_decode, kv):
+    """The run's workload by its own name: S1 is 128 + 128, the long-context
+    workload 2048 + 256; anything else is named by its sizes only."""
+    shape = "Qwen2.5-7B" if is7b else "Qwen2.5-1.5B"
+    name = {(128, 128): " S1", (2048, 256): " long-context"}.get((n_prompt, n_decode), "")
+    return (f"{shape}-shape{name}: {n_prompt} prompt ids prefilled + {n_decode} greedy decode "
+            f"steps, batch 1, {kv} KV cache")
+
+
 def bench_prompt(shape, n):
     return np.random.default_rng(2024).integers(0, shape.vocab, n).astype(np.uint32)
 
@@ -447,8 +456,7 @@ def main():
         "vs_baseline": None if is7b else round(decode_tok_s / REF_CPU_DECODE_TOK_S, 2),
         "dtype": "bf16", "data": "synthetic: random-init N(0,0.02) bf16 weights (seed 0), "
                                  "uniform prompt ids (seed 2024)",
-        "config": {"workload": f"{'Qwen2.5-7B' if is7b else 'Qwen2.5-1.5B'}-shape S1: {args.prompt} prompt ids prefilled + "
-                               f"{args.decode} greedy decode steps, batch 1",
+        "config": {"workload": workload_name(is7b, args.prompt, args.decode, args.kv),
                    "prompt_ids": args.prompt, "decode_steps": args.decode, "batch": 1,
                    "max_seq": max_seq, "kv_cache": args.kv,
                    "accumulate": "f32 accumulate over bf16 weights; activations enter the "

@@ -133,6 +133,38 @@ int myos_gqa_attn_f32(float *y, size_t y_len, const float *q, size_t q_len, cons
 int myos_swiglu_mul_f32(float *h, size_t h_len, const float *gate, size_t gate_len,
                         const float *up, size_t up_len, myos_stream_t stream);
 
+/* swiglu_bf16, crates/tensor_core/src/swiglu.rs:184-213: gate = W_g x,
+ * up = W_u x (W_g, W_u [intermediate, hidden] bf16), h = silu(gate) * up,
+ * y = W_d h (W_d [hidden, intermediate]); gate / up / h are the caller's
+ * scratch (the reference's argument order: activations, weights, scratch,
+ * shape). hidden or intermediate zero, or any length mismatch -> SHAPE. */
+int myos_swiglu_bf16(float *y, size_t y_len, const float *x, size_t x_len, const uint16_t *gate_w,
+                     size_t gate_w_len, const uint16_t *up_w, size_t up_w_len, const uint16_t *down_w,
+                     size_t down_w_len, float *gate, size_t gate_len, float *up, size_t up_len,
+                     float *h, size_t h_len, size_t hidden, size_t intermediate,
+                     myos_stream_t stream);
+
+/* silu_f32, crates/tensor_core/src/swiglu.rs:113-115, elementwise on the
+ * device: y[i] = z[i] / (1 + expf(-z[i])). y_len != z_len -> SHAPE. */
+int myos_silu_f32(float *y, size_t y_len, const float *z, size_t z_len, myos_stream_t stream);
+
+/* rmsnorm_f32, crates/tensor_core/src/bf16.rs:200-216: rmsnorm_bf16_weight
+ * with an f32 gamma. n == 0 or length mismatch -> SHAPE. */
+int myos_rmsnorm_f32(float *y, size_t y_len, const float *weight, size_t weight_len, const float *x,
+                     size_t x_len, float eps, myos_stream_t stream);
+
+/* rope_inv_freqs, crates/tensor_core/src/rope.rs:89-98: inv_freq[i] =
+ * 1 / powf(theta, f32(2 i) / f32(head_dim)) into DEVICE memory, evaluated on
+ * the host with the reference's expression (as every RoPE table here is).
+ * head_dim zero or odd, or len != head_dim / 2 -> SHAPE. */
+int myos_rope_inv_freqs(float *inv_freq, size_t len, size_t head_dim, float theta,
+                        myos_stream_t stream);
+
+/* attn_scale_f32, crates/tensor_core/src/gqa.rs:158-163: *out = 1 /
+ * sqrtf(head_dim) (host), the factor the attention kernels apply to each
+ * finished dot. head_dim == 0 -> SHAPE. */
+int myos_attn_scale_f32(size_t head_dim, float *out);
+
 /* greedy_token, crates/model_core/src/lib.rs:157-167: first index of the
  * strict maximum (ties -> lowest index, NaN never wins, all -inf/NaN -> 0).
  * Two-pass block argmax; the u32 result is written to DEVICE memory *out. */
@@ -190,6 +222,18 @@ int myos_greedy_decode(myos_model *m, size_t steps, uint32_t *out);
  * same ids. Checks before any launch: ids[s] >= vocab -> TOKEN; steps past
  * max_seq -> KV_FULL (nothing runs). */
 int myos_decode_forced(myos_model *m, const uint32_t *ids, size_t steps, uint32_t *argmax_out);
+
+/* attention_layer, crates/model_core/src/attn_wire.rs:207-313, on the model's
+ * weights: residual += o_proj(attention(proj_in)) for `layer` at `pos`, where
+ * proj_in (the caller's normed vector) feeds q/k/v (+ bias, RoPE at pos) and
+ * the layer's K/V row is stored at pos; the cursor does not move. residual
+ * and proj_in are HOST vectors of len == hidden floats. Checks before any
+ * launch: len -> SHAPE; layer >= layers -> KV_RANGE (KvError::Range); pos !=
+ * cursor -> POSITION; pos >= max_seq -> KV_FULL. */
+int myos_attention_layer(myos_model *m, size_t layer, size_t pos, float *residual,
+                         const float *proj_in, size_t len);
+/* KvCache::advance, kv_cache.rs:226-232: cursor += 1; at max_seq -> KV_FULL. */
+int myos_kv_advance(myos_model *m);
 
 size_t myos_cache_len(const myos_model *m);        /* KvCache::len */
 /* KvCache::clear (kv_cache.rs:234-237): cursor back to 0, slots kept. */

@@ -90,6 +90,33 @@ def test_small_op_checks(L):
     s = L.myos_swiglu_mul_f32
     assert s(DUMMY, 0, DUMMY, 0, DUMMY, 0, None) == myos.E_SHAPE
     assert s(DUMMY, 2, DUMMY, 4, DUMMY, 4, None) == myos.E_SHAPE
+    # swiglu_bf16 (swiglu.rs:184-213): y, x [hidden]; gate/up/h [inter];
+    # weights inter x hidden each; any mismatch or a zero dimension -> Shape
+    sw = L.myos_swiglu_bf16
+    ok = [2, 2, 6, 6, 6, 3, 3, 3]  # y, x, gate_w, up_w, down_w, gate, up, h for 2 x 3
+    def call(lens, hid=2, inter=3):
+        flat = [v for n in lens for v in (DUMMY, n)]
+        return sw(*flat, hid, inter, None)
+    for i in range(8):
+        bad = list(ok)
+        bad[i] += 1
+        assert call(bad) == myos.E_SHAPE, i
+    assert call(ok, 0, 3) == myos.E_SHAPE and call(ok, 2, 0) == myos.E_SHAPE
+    assert L.myos_silu_f32(DUMMY, 2, DUMMY, 3, None) == myos.E_SHAPE
+    assert L.myos_silu_f32(DUMMY, 0, DUMMY, 0, None) == myos.OK
+    rf = L.myos_rmsnorm_f32
+    assert rf(DUMMY, 0, DUMMY, 0, DUMMY, 0, 1e-6, None) == myos.E_SHAPE
+    assert rf(DUMMY, 2, DUMMY, 1, DUMMY, 2, 0.0, None) == myos.E_SHAPE
+    ri = L.myos_rope_inv_freqs
+    assert ri(DUMMY, 2, 3, 1e6, None) == myos.E_SHAPE   # odd head_dim
+    assert ri(DUMMY, 3, 4, 1e6, None) == myos.E_SHAPE   # len != head_dim / 2
+    assert ri(DUMMY, 0, 0, 1e6, None) == myos.E_SHAPE
+    import ctypes
+    sc = ctypes.c_float()
+    assert L.myos_attn_scale_f32(0, ctypes.byref(sc)) == myos.E_SHAPE
+    assert L.myos_attn_scale_f32(128, ctypes.byref(sc)) == myos.OK
+    import oracle
+    assert np.float32(sc.value) == oracle.attn_scale_f32(128)  # gqa.rs:158-163 bits
 
 
 def test_gqa_checks(L):

@@ -60,6 +60,7 @@ def built():
     (["--teacher-forced", "--block-fixture"], "--teacher-forced needs --ref-ids"),
     (["--gaps", "--gaps"], "--gaps was given more than once"),
     (["--kv", "f16"], "--kv needs f32 or bf16"),
+    (["--decode-path", "wide"], "--decode-path needs auto, kernels, persistent or streamed"),
 ])
 def test_argument_errors(args, msg):
     r = run(*args)
@@ -146,6 +147,24 @@ def test_weights_cli_qwen15(tmp_path, qwen15):
         for blk in iter(lambda: fh.read(1 << 24), b""):
             h.update(blk)
     assert m["model_sha256"] == f["model_sha256"] == h.hexdigest()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("path", ["streamed", "kernels", "persistent"])
+def test_cli_decode_path_recorded(tmp_path, qwen15, path):
+    """--decode-path picks each decode path by name, and run_fingerprint.json
+    and metrics.json name the path that ran (the streamed cooperative kernel
+    is the 7B shape's default, so a 7B run records it too)."""
+    prompt = [int(v) for v in np.random.default_rng(9).integers(0, 151936, 8)]
+    (tmp_path / "p.txt").write_text(" ".join(map(str, prompt)) + "\n")
+    fp = tmp_path / "fp"
+    r = run("--weights", qwen15, "--prompt-ids", str(tmp_path / "p.txt"), "--steps", "3",
+            "--decode-path", path, "--no-hash", "--fingerprint-dir", str(fp))
+    assert r.returncode == 0, r.stderr
+    f = json.loads((fp / "run_fingerprint.json").read_text())
+    m = json.loads((fp / "metrics.json").read_text())
+    assert f["decode_path"] == m["decode_path"] == path
+    assert m["model_sha256"] is None
 
 
 @pytest.mark.gpu

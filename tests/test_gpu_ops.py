@@ -146,6 +146,64 @@ def test_bias_embed_rmsnorm_swiglu():
     assert max_rel(host(h), oracle.swiglu_mul_f32(gate, up)) < 1e-6
 
 
+@pytest.mark.parametrize("hidden,inter", [(1536, 8960), (48, 100), (37, 19)])
+def test_swiglu_bf16_vs_oracle(hidden, inter):
+    # swiglu.rs:184-213 composed on the oracle: gate, up, h, y
+    rng = np.random.default_rng(hidden + inter)
+    x = rng.standard_normal(hidden).astype(np.float32)
+    wg, wu, wd = rand_w(rng, inter, hidden), rand_w(rng, inter, hidden), rand_w(rng, hidden, inter)
+    g_ref = oracle.gemv_bf16(wg, x, inter, hidden, threads=8)
+    u_ref = oracle.gemv_bf16(wu, x, inter, hidden, threads=8)
+    h_ref = oracle.swiglu_mul_f32(g_ref, u_ref)
+    y_ref = oracle.gemv_bf16(wd, h_ref, hidden, inter, threads=8)
+    y = torch.zeros(hidden, device=DEV)
+    g, u, h = (torch.zeros(inter, device=DEV) for _ in range(3))
+    myos.swiglu_bf16(y, dev(x), dev(wg, torch.int16), dev(wu, torch.int16), dev(wd, torch.int16),
+                     g, u, h, hidden, inter)
+    assert max_rel(host(g), g_ref) < 1e-5 and max_rel(host(u), u_ref) < 1e-5
+    assert max_rel(host(h), h_ref) < 1e-5
+    assert max_rel(host(y), y_ref) < 1e-4
+    # a shape error leaves every output as it was
+    y.fill_(7.0)
+    with pytest.raises(myos.MyosError) as e:
+        myos.swiglu_bf16(y, dev(x), dev(wg, torch.int16), dev(wu, torch.int16),
+                         dev(wd[:-1], torch.int16), g, u, h, hidden, inter)
+    assert e.value.kind == "Shape" and bool((y == 7.0).all())
+
+
+def test_silu_rmsnorm_f32_inv_freqs_scale():
+    # silu_f32 (swiglu.rs:113-115) elementwise, against the oracle's libm silu
+    # and the reference's bits (swiglu.rs:362-377: silu(1) = 0x3F3B26A8)
+    z0 = np.concatenate([np.float32([1.0, 0.0, -1.0, 20.0, -20.0, 1e-3]),
+                         np.random.default_rng(4).standard_normal(4000).astype(np.float32) * 6])
+    y = torch.zeros(z0.size, device=DEV)
+    myos.silu_f32(y, dev(z0))
+    got = host(y)
+    ref = np.array([oracle.silu_f32(float(v)) for v in z0], np.float32)
+    assert got[0].view(np.uint32) == 0x3F3B26A8
+    assert np.all(np.abs(got - ref) <= 4 * 2.0 ** -24 * np.maximum(np.abs(ref), 2.0 ** -126))
+    # rmsnorm_f32 (bf16.rs:200-216) against the reference's f32 expression
+    rng = np.random.default_rng(6)
+    x = rng.standard_normal(1536).astype(np.float32)
+    w = rng.uniform(0.5, 1.5, 1536).astype(np.float32)
+    yr = torch.zeros(1536, device=DEV)
+    myos.rmsnorm_f32(yr, dev(w), dev(x), np.float32(1e-6))
+    inv = np.float32(1) / np.float32(np.sqrt(np.float32(np.sum(x.astype(np.float64) ** 2) / 1536)
+                                             + np.float32(1e-6)))
+    assert max_rel(host(yr), w * (x * inv)) < 1e-6
+    yr = torch.zeros(4, device=DEV)
+    myos.rmsnorm_f32(yr, dev(np.float32([1.5, 4.0, -2.0, 0.5])), dev(np.float32([8, 0, 0, 0])), 0.0)
+    assert list(host(yr)) == [3.0, 0.0, 0.0, 0.0]
+    # rope_inv_freqs (rope.rs:89-98) bit for bit with the oracle (both libm powf)
+    for d in (2, 64, 128):
+        t = torch.zeros(d // 2, device=DEV)
+        myos.rope_inv_freqs(t, d, THETA)
+        assert list(host(t).view(np.uint32)) == list(oracle.rope_inv_freqs(d, THETA).view(np.uint32))
+    # attn_scale_f32 (gqa.rs:158-163)
+    for d in (1, 32, 128):
+        assert np.float32(myos.attn_scale_f32(d)) == oracle.attn_scale_f32(d)
+
+
 @pytest.mark.parametrize("pos,d,heads", [(1, 2, 1), (3, 4, 2), (8, 128, 12), (2303, 128, 2),
                                          (0, 128, 12)])
 def test_rope(pos, d, heads):
