@@ -21,8 +21,28 @@
  *   orc_gqa_attn_f32         gqa.rs:357-608 bits
  *   orc_silu_f32 / swiglu    swiglu.rs:362-452 bits
  *   orc_greedy_token         model_core/src/lib.rs:157-167 spec (ties, NaN)
+ *   orc_attention_layer      attn_wire.rs:450-704 hand fixtures (grouped step, bias after
+ *                            the GEMV, second-token mix, RoPE on k not v)
  *   orc_model_*              qwen25_block.rs:1011-1071 block fixture [1,2,0,-1] / [1,1,1,1];
- *                            :1423-1478 chunk prefill == serial forward bits
+ *                            :1423-1478 chunk prefill == serial forward bits; block errors
+ *                            leave the cursor; two layers advance once per token; untied
+ *                            head copy == tied; the post-attention norm feeds the MLP;
+ *                            the MLP residual changes the logits
+ *   orc_model_* (wiring)     an independent float64 numpy Qwen2 forward written from the
+ *                            architecture's definition (tests/qwen2_textbook.py) agrees
+ *                            on random small models
+ *   orc_model_* (mutations)  tests/test_oracle_mutations.py rebuilds this file with one
+ *                            plausible wiring mistake each (MLP norm reads ln1, MLP
+ *                            residual dropped, KV store ignores the layer, untied head
+ *                            ignored, prefill attends layer 0's cache, RoPE on v, and the
+ *                            three bf16-cache mistakes below) and requires a pin to fail
+ *   orc_round_bf16           closed forms: representable values unchanged, halfway cases
+ *                            to even, above / below half, overflow to inf, NaN kept,
+ *                            tiny denormals to zero
+ *   orc_set_kv_bf16          hand fixture whose hidden state depends only on how v is
+ *                            rounded (1 + 3*2^-8 -> 1 + 2^-6, 1 + 2^-9 -> 1); every
+ *                            layer-0 cache row equals RNE of the f32 mode's row;
+ *                            chunk prefill == serial decode bits in bf16 mode
  */
 #ifndef MYOS_ORACLE_H
 #define MYOS_ORACLE_H
