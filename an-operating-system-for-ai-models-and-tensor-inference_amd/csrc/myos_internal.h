@@ -211,11 +211,18 @@ size_t persist_pr_words(int H, int nq);
 bool persist_supported(int H, int I, int qdim, int d, int gq);
 bool persist_device_ok(const PersistArgs &a);  // shape, LDS and the current device fit
 hipError_t launch_decode_persistent(const PersistArgs &a, hipStream_t s);
+// first-use set-up of the instantiation a launch with these arguments takes
+// (launches do it themselves when it has not been done)
+hipError_t persist_prepare(const PersistArgs &a);
+// one empty cooperative launch on s (and a wait for it): the runtime's set-up
+// for a stream's first cooperative launch
+hipError_t coop_warm_launch(hipStream_t s);
 // the streamed cooperative kernel, for layers larger than the chip holds
 bool wide_supported(int H, int I, int qdim, int d, int gq, int max_seq);
 size_t wide_buffer_floats(int H, int I, int nq, int d, int max_seq);
 bool wide_device_ok(const PersistArgs &a);
 hipError_t launch_decode_wide(const PersistArgs &a, hipStream_t s);
+hipError_t wide_prepare(const PersistArgs &a);
 
 // dst[c][r] = src[r][c] for a [rows, cols] matrix of 32-bit words
 hipError_t launch_transpose_u32(uint32_t *dst, const uint32_t *src, int rows, int cols,

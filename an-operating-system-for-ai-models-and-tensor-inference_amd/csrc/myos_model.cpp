@@ -498,6 +498,11 @@ int setup_persistent(myos_model *m) {
   a.state = m->state;
   a.out_ids = m->out_ids;
   a.force = nullptr;
+  // the kernels' first-use set-up (code object load, LDS limit) belongs to
+  // load time, not to the first decode call's timed region
+  if (reg) HIP_TRY(persist_prepare(a));
+  if (wide) HIP_TRY(wide_prepare(a));
+  HIP_TRY(coop_warm_launch(m->stream));
   m->persist_ok = reg;
   m->wide_ok = wide;
   return MYOS_OK;

@@ -2546,13 +2546,14 @@ bool persist_device_ok(const PersistArgs &a) {
   return coop != 0 && cus >= NB;
 }
 
-hipError_t launch_decode_persistent(const PersistArgs &a, hipStream_t s) {
-  if (!persist_supported(a.H, a.I, a.nq * a.d, a.d, a.nq / a.nkv)) return hipErrorInvalidValue;
-  if (a.steps == 0) return hipSuccess;
-  if (a.pos0 + a.steps > (uint32_t)a.max_seq) return hipErrorInvalidValue;
-  PersistArgs args = a;
-  const size_t smem = persist_lds(args);
-  if (smem > kMaxLds) return hipErrorInvalidValue;
+// The instantiation a launch with these arguments runs, and its first-use
+// set-up: the dynamic LDS limit, and the function's attributes, whose query
+// loads the kernel's code object onto the device. Done once per
+// instantiation; launch_decode_persistent does it on its first call, and
+// persist_prepare lets a caller do it before it starts timing (a first
+// launch otherwise spends about 6 ms of host time between a stream event
+// recorded before it and the kernel's start).
+static hipError_t persist_fn(const PersistArgs &a, const void **out) {
   const bool qwen15 = a.H == 1536 && a.I == 8960 && a.V == 151936 && a.nq == 12 && a.nkv == 2 &&
                       a.d == 128;
   const bool kb = a.kv_bf16 != 0;
@@ -2575,8 +2576,42 @@ hipError_t launch_decode_persistent(const PersistArgs &a, hipStream_t s) {
   if (!attr_set[which]) {
     hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxLds);
     if (e != hipSuccess) return e;
+    hipFuncAttributes fa;
+    e = hipFuncGetAttributes(&fa, fn);
+    if (e != hipSuccess) return e;
     attr_set[which] = true;
   }
+  *out = fn;
+  return hipSuccess;
+}
+
+hipError_t persist_prepare(const PersistArgs &a) {
+  if (!persist_supported(a.H, a.I, a.nq * a.d, a.d, a.nq / a.nkv)) return hipErrorInvalidValue;
+  const void *fn = nullptr;
+  return persist_fn(a, &fn);
+}
+
+// An empty kernel, launched cooperatively with the decode kernels' grid: the
+// runtime's own set-up for a stream's first cooperative launch (about 4 ms of
+// host time before the kernel starts, measured on MI355X) then happens here.
+__global__ void __launch_bounds__(NT) coop_warm_kernel() {}
+
+hipError_t coop_warm_launch(hipStream_t s) {
+  hipError_t e = hipLaunchCooperativeKernel((const void *)coop_warm_kernel, dim3(NB), dim3(NT), nullptr, 0, s);
+  if (e != hipSuccess) return e;
+  return hipStreamSynchronize(s);
+}
+
+hipError_t launch_decode_persistent(const PersistArgs &a, hipStream_t s) {
+  if (!persist_supported(a.H, a.I, a.nq * a.d, a.d, a.nq / a.nkv)) return hipErrorInvalidValue;
+  if (a.steps == 0) return hipSuccess;
+  if (a.pos0 + a.steps > (uint32_t)a.max_seq) return hipErrorInvalidValue;
+  PersistArgs args = a;
+  const size_t smem = persist_lds(args);
+  if (smem > kMaxLds) return hipErrorInvalidValue;
+  const void *fn = nullptr;
+  hipError_t e = persist_fn(args, &fn);
+  if (e != hipSuccess) return e;
   void *params[] = {&args};
   return hipLaunchCooperativeKernel(fn, dim3(NB), dim3(NT), params, (unsigned)smem, s);
 }
@@ -2619,10 +2654,9 @@ bool wide_device_ok(const PersistArgs &a) {
   return coop != 0 && cus >= NB;
 }
 
-hipError_t launch_decode_wide(const PersistArgs &a, hipStream_t s) {
-  if (!wide_supported(a.H, a.I, a.nq * a.d, a.d, a.nq / a.nkv, a.max_seq)) return hipErrorInvalidValue;
-  if (a.steps == 0) return hipSuccess;
-  if (a.pos0 + a.steps > (uint32_t)a.max_seq) return hipErrorInvalidValue;
+// the streamed kernel's instantiation for these arguments and its first-use
+// set-up (as persist_fn)
+static hipError_t wide_fn(const PersistArgs &a, const void **out) {
   const size_t smem = wide_lds_bytes(a.d, a.max_seq);
   const bool narrow = a.H <= 64 * 8 * 3 && a.nq * a.d <= 64 * 8 * 3;
   const bool kb = a.kv_bf16 != 0;
@@ -2637,11 +2671,32 @@ hipError_t launch_decode_wide(const PersistArgs &a, hipStream_t s) {
   if (attr_set[which] < smem) {
     hipError_t e = hipFuncSetAttribute(fns[which], hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
     if (e != hipSuccess) return e;
+    hipFuncAttributes fa;
+    e = hipFuncGetAttributes(&fa, fns[which]);
+    if (e != hipSuccess) return e;
     attr_set[which] = smem;
   }
+  *out = fns[which];
+  return hipSuccess;
+}
+
+hipError_t wide_prepare(const PersistArgs &a) {
+  if (!wide_supported(a.H, a.I, a.nq * a.d, a.d, a.nq / a.nkv, a.max_seq)) return hipErrorInvalidValue;
+  const void *fn = nullptr;
+  return wide_fn(a, &fn);
+}
+
+hipError_t launch_decode_wide(const PersistArgs &a, hipStream_t s) {
+  if (!wide_supported(a.H, a.I, a.nq * a.d, a.d, a.nq / a.nkv, a.max_seq)) return hipErrorInvalidValue;
+  if (a.steps == 0) return hipSuccess;
+  if (a.pos0 + a.steps > (uint32_t)a.max_seq) return hipErrorInvalidValue;
+  const void *fn = nullptr;
+  hipError_t e = wide_fn(a, &fn);
+  if (e != hipSuccess) return e;
+  const size_t smem = wide_lds_bytes(a.d, a.max_seq);
   PersistArgs args = a;
   void *params[] = {&args};
-  return hipLaunchCooperativeKernel(fns[which], dim3(NB), dim3(NT), params, (unsigned)smem, s);
+  return hipLaunchCooperativeKernel(fn, dim3(NB), dim3(NT), params, (unsigned)smem, s);
 }
 
 }  // namespace myos
