@@ -574,9 +574,25 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
   constexpr bool HA = AM == 2;
   const int NA = HA ? 2 * nq : 0, NBW = NB - NA;
   const bool is_att = HA && wg >= NBW;
-  const int ah = HA ? max(wg - NBW, 0) >> 1 : 0;  // q head
-  const int avh = HA ? max(wg - NBW, 0) & 1 : 0;  // value half
-  const int ag = ah / gq;                          // its kv head
+  // attention workgroup i = wg - NBW takes q head ah, value half avh. The
+  // dispatcher deals workgroups to the 8 XCDs round robin (XCD = wg % 8),
+  // and each XCD's L2 fetches the cached rows its workgroups read: with 12 q
+  // heads over 2 kv heads, kv head g goes to XCDs 4 g .. 4 g + 3 (3
+  // workgroups each), so its K rows are fetched by 4 L2s and each value half
+  // by 2, where i -> (i / 2, i % 2) spreads every kv head over all 8.
+  int ah = 0, avh = 0;
+  if (HA) {
+    const int i = max(wg - NBW, 0);
+    if (nq == 12 && nkv == 2 && NBW % 8 == 0) {
+      const int x = i & 7, li = (i >> 3) * 4 + (x & 3);
+      ah = (x >> 2) * 6 + (li >> 1);
+      avh = li & 1;
+    } else {
+      ah = i >> 1;
+      avh = i & 1;
+    }
+  }
+  const int ag = ah / gq;  // its kv head
   // ownership
   const int qper = (((qkv_rows + NBW - 1) / NBW) + 1) & ~1;
   const int q0 = wg < NBW ? wg * qper : qkv_rows, q1 = min(q0 + qper, qkv_rows);
