@@ -32,6 +32,7 @@ sys.path.insert(0, ROOT)
 myos = importlib.import_module("an-operating-system-for-ai-models-and-tensor-inference_amd")
 
 HBM_PEAK = 8.0e12  # MI355X HBM3E, bytes/s
+MFMA_BF16_PEAK = 2.5e15  # MI355X dense bf16 MFMA, FLOP/s
 REF_CPU_DECODE_TOK_S = 15.4880  # reference S1 decode tok/s, 8 threads
 METRIC = "decode tok/s + % HBM roofline, Qwen2.5-1.5B-shape bf16 bs=1; prefill tok/s"
 
@@ -64,6 +65,34 @@ def weight_bytes(s) -> int:
 
 def kv_bytes_per_token(s, seq, kv_bytes) -> int:
     return s.num_layers * 2 * s.num_kv_heads * s.head_dim * seq * kv_bytes
+
+
+def prefill_flops(s, n) -> float:
+    """Algorithmic FLOPs of prefilling n ids from an empty cache: every
+    projection as a GEMM over the n rows, causal attention (q.k and p.v over
+    the keys each query sees) and the head for the last id only."""
+    qd, kvd = s.num_q_heads * s.head_dim, s.num_kv_heads * s.head_dim
+    per_row = s.hidden * (qd + 2 * kvd) + qd * s.hidden + 3 * s.hidden * s.intermediate
+    attn = 2.0 * s.num_q_heads * s.head_dim * (n * (n + 1) / 2.0)
+    return s.num_layers * (2.0 * n * per_row + 2.0 * attn) + 2.0 * s.vocab * s.hidden
+
+
+def prefill_leg(path, shape, kv, n, reps=3):
+    """The MFMA prefill alone on n seeded ids (one warm-up, median of reps
+    device times), from an empty cache of max_seq n."""
+    ids = np.random.default_rng(2048).integers(0, shape.vocab, n).astype(np.uint32)
+    ms = []
+    with myos.Model.open(path, shape, kv, n) as g:
+        for r in range(reps + 1):
+            g.cache_clear()
+            g.prefill(ids)
+            if r:
+                ms.append(g.last_prefill_ms())
+    t = float(np.median(ms))
+    fl = prefill_flops(shape, n)
+    return {"prompt_ids": n, "device_ms": round(t, 3), "tok_s": round(n / (t * 1e-3), 1),
+            "flops_alg": fl, "mfma_frac_alg": round(fl / (t * 1e-3) / MFMA_BF16_PEAK, 4),
+            "runs": [round(x, 3) for x in ms]}
 
 
 def gemv_microbench(reps=5):
@@ -249,6 +278,8 @@ def main():
     ap.add_argument("--decode-path", choices=["auto", "kernels", "persistent", "streamed"],
                     default="auto")
     ap.add_argument("--no-gemv-microbench", action="store_true")
+    ap.add_argument("--no-prefill-2048", action="store_true",
+                    help="skip the 2048-id prefill-only leg")
     ap.add_argument("--shape", choices=["qwen2.5-1.5b", "qwen2.5-7b"], default="qwen2.5-1.5b",
                     help="model shape (the headline metric is quoted on qwen2.5-1.5b)")
     ap.add_argument("--host-legs", metavar="DIR", help=argparse.SUPPRESS)
@@ -427,6 +458,11 @@ def main():
                     "algorithmic_bytes": dom["bytes"]}
     m.close()
 
+    pf_long = None if args.no_prefill_2048 else prefill_leg(path, shape, kv, 2048)
+    if pf_long:
+        log(f"prefill 2048 ids: {pf_long['device_ms']} ms ({pf_long['tok_s']} tok/s, "
+            f"{pf_long['mfma_frac_alg']} of the bf16 MFMA peak counted algorithmically)")
+
     micro = None if args.no_gemv_microbench else gemv_microbench()
     if micro:
         log("gemv microbench: " + ", ".join(f"{n} {v['avg_us']}us {v['GBps']}GB/s"
@@ -476,7 +512,7 @@ def main():
                             "frac": round(decode_frac, 4)},
         "prefill_roofline": pf_roof,
         "roofline": roofline, "parity": parity, "arena": arena,
-        "per_kernel_path": kernels, "gemv_microbench": micro,
+        "per_kernel_path": kernels, "prefill_2048": pf_long, "gemv_microbench": micro,
         "t_load_s": round(t_load, 2),
         "cpu_baseline": cpu,
     }
