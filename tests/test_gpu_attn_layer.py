@@ -1,9 +1,12 @@
 """attention_layer (attn_wire.rs:207-313) through the model tier's
 myos_attention_layer, on the reference's own hand fixtures
-(attn_wire.rs:450-704, restated on the oracle in test_oracle_golden.py):
+(attn_wire.rs:450-836, restated on the oracle in test_oracle_golden.py):
 grouped heads over one step, biases added after the GEMV, a second token
-mixing two cached rows, and RoPE applied to K but not V. Every expected value
-is the reference's hard-coded answer, exact in any summation order."""
+mixing two cached rows, RoPE applied to K but not V, two layers storing their
+rows before one cursor advance, and errors that leave the residual and the
+cache untouched. Every expected value is the reference's hard-coded answer,
+exact in any summation order."""
+import ctypes
 import importlib
 
 import numpy as np
@@ -18,25 +21,31 @@ pytestmark = pytest.mark.gpu
 
 
 def attn_model(tmp_path, hidden, nq, nkv, d, proj, max_seq):
-    s = shape_dict(hidden, nq, nkv, d, 2, 4, 1, 0.0)
+    """A model whose layer l has the attention projections proj[l] (one dict
+    or a list of them) and a zero MLP."""
+    projs = proj if isinstance(proj, list) else [proj]
+    s = shape_dict(hidden, nq, nkv, d, 2, 4, len(projs), 0.0)
     t = {"model.embed_tokens.weight": bits(np.zeros(4 * hidden), (4, hidden)),
          "model.norm.weight": bits(np.ones(hidden))}
-    qd, kd, p = nq * d, nkv * d, "model.layers.0."
-    t[p + "input_layernorm.weight"] = bits(np.ones(hidden))
-    t[p + "post_attention_layernorm.weight"] = bits(np.ones(hidden))
-    t[p + "self_attn.q_proj.weight"] = bits(proj["q_w"], (qd, hidden))
-    t[p + "self_attn.q_proj.bias"] = bits(proj["q_b"])
-    t[p + "self_attn.k_proj.weight"] = bits(proj["k_w"], (kd, hidden))
-    t[p + "self_attn.k_proj.bias"] = bits(proj["k_b"])
-    t[p + "self_attn.v_proj.weight"] = bits(proj["v_w"], (kd, hidden))
-    t[p + "self_attn.v_proj.bias"] = bits(proj["v_b"])
-    t[p + "self_attn.o_proj.weight"] = bits(proj["o_w"], (hidden, qd))
-    for n in ("gate", "up"):
-        t[p + f"mlp.{n}_proj.weight"] = bits(np.zeros(2 * hidden), (2, hidden))
-    t[p + "mlp.down_proj.weight"] = bits(np.zeros(2 * hidden), (hidden, 2))
+    qd, kd = nq * d, nkv * d
+    for l, pr in enumerate(projs):
+        p = f"model.layers.{l}."
+        t[p + "input_layernorm.weight"] = bits(np.ones(hidden))
+        t[p + "post_attention_layernorm.weight"] = bits(np.ones(hidden))
+        t[p + "self_attn.q_proj.weight"] = bits(pr["q_w"], (qd, hidden))
+        t[p + "self_attn.q_proj.bias"] = bits(pr["q_b"])
+        t[p + "self_attn.k_proj.weight"] = bits(pr["k_w"], (kd, hidden))
+        t[p + "self_attn.k_proj.bias"] = bits(pr["k_b"])
+        t[p + "self_attn.v_proj.weight"] = bits(pr["v_w"], (kd, hidden))
+        t[p + "self_attn.v_proj.bias"] = bits(pr["v_b"])
+        t[p + "self_attn.o_proj.weight"] = bits(pr["o_w"], (hidden, qd))
+        for n in ("gate", "up"):
+            t[p + f"mlp.{n}_proj.weight"] = bits(np.zeros(2 * hidden), (2, hidden))
+        t[p + "mlp.down_proj.weight"] = bits(np.zeros(2 * hidden), (hidden, 2))
     path = str(tmp_path / "attn.safetensors")
     write_safetensors(path, t)
-    shape = myos.make_shape(hidden, nq, nkv, d, 2, 4, 1, rms_eps=0.0, rope_theta=float(THETA))
+    shape = myos.make_shape(hidden, nq, nkv, d, 2, 4, len(projs), rms_eps=0.0,
+                            rope_theta=float(THETA))
     return myos.Model.open(path, shape, myos.KV_F32, max_seq)
 
 
@@ -106,3 +115,42 @@ def test_rope_k_not_v(tmp_path):
         rot = oracle.rope_f32_inplace([1.0, 0.0], 1, 2, THETA)[1]
         assert list(m.kv(0, 0, 1)[0].view(np.uint32)) == list(np.float32(rot).view(np.uint32))
         assert list(m.kv(0, 0, 1)[1]) == [4.0, 8.0]
+
+
+def test_two_layers_store_then_one_advance(tmp_path):
+    # attn_wire.rs:706-765: each layer stores its own V row at position 0,
+    # the cursor moves only on the one advance
+    proj = [dict(q_w=np.zeros(16), q_b=np.zeros(4), k_w=np.zeros(8), k_b=np.zeros(2),
+                 v_w=np.zeros(8), v_b=vb, o_w=np.eye(4).ravel()) for vb in ([1.0, 0.0], [0.0, 1.0])]
+    with attn_model(tmp_path, 4, 2, 1, 2, proj, 2) as m:
+        r = np.zeros(4, np.float32)
+        r = m.attention_layer(0, 0, r, r.copy())
+        assert list(r) == [1, 0, 1, 0] and m.cache_len() == 0
+        r = m.attention_layer(1, 0, r, r.copy())
+        assert list(r) == [1, 1, 1, 1] and m.cache_len() == 0
+        assert list(m.kv(0, 0, 0)[1]) == [1, 0] and list(m.kv(1, 0, 0)[1]) == [0, 1]
+        m.kv_advance()
+        assert m.cache_len() == 1 and list(m.kv(0, 0, 0)[1]) == [1, 0]
+
+
+def test_errors_leave_residual_and_cache(tmp_path):
+    # attn_wire.rs:767-836 through the C entry point itself: a rejected call
+    # writes neither the caller's residual nor the cache, nor moves the cursor
+    # (the weight errors of that test surface at model open here, covered by
+    # test_abi's preflight cases)
+    proj = dict(q_w=np.zeros(16), q_b=np.zeros(4), k_w=np.zeros(8), k_b=[1.0, 0.0],
+                v_w=np.zeros(8), v_b=[4.0, 8.0], o_w=np.eye(4).ravel())
+    with attn_model(tmp_path, 4, 2, 1, 2, proj, 2) as m:
+        res = np.full(4, 7.0, np.float32)
+        x = np.array([1, 0, 0, 0], np.float32)
+        vp = ctypes.c_void_p
+        call = lambda layer, pos, n: myos.lib().myos_attention_layer(
+            m._h, layer, pos, res.ctypes.data_as(vp), x.ctypes.data_as(vp), n)
+        for (layer, pos, n), code in (((0, 1, 4), myos.E_POSITION), ((1, 0, 4), myos.E_KV_RANGE),
+                                      ((0, 0, 3), myos.E_SHAPE)):
+            assert call(layer, pos, n) == code
+            assert list(res) == [7, 7, 7, 7] and m.cache_len() == 0
+            assert list(m.kv(0, 0, 0)[0]) == [0, 0] and list(m.kv(0, 0, 0)[1]) == [0, 0]
+        # the same call at the cursor then succeeds and writes both
+        assert call(0, 0, 4) == 0
+        assert list(res) == [11, 15, 11, 15] and list(m.kv(0, 0, 0)[0]) == [1, 0]
