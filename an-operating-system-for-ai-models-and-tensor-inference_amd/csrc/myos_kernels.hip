@@ -2734,9 +2734,14 @@ using PfW256 = PfCfg<2, 2, 2, 4>;
 // 128 x 192 with eight waves (32 x 96 each): 8 N tiles of a 1536-wide
 // projection, so 16 M tiles x 2 splits fill the 256 CUs exactly
 using PfW192 = PfCfg<1, 3, 4, 2>;
-constexpr int kPfCfgs = 6;
-constexpr int kPfPlanCfgs = 4;  // the cost model's candidates (the wider ones are picked by shape)
-constexpr int kPfBN[kPfCfgs] = {PfT32::BN, PfT64::BN, PfT128::BN, PfT256::BN, PfW256::BN, PfW192::BN};
+// Short prompts (at most 128 rows): 64-row tiles halve the activation bytes
+// each workgroup pulls per weight byte. 64 x 64 with four waves for the
+// narrow projections, 64 x 128 with eight waves for gate/up.
+using PfS64 = PfCfg<1, 1, 2, 2>;
+using PfS128 = PfCfg<1, 1, 2, 4>;
+constexpr int kPfCfgs = 8;
+constexpr int kPfPlanCfgs = 4;  // the cost model's candidates (the others are picked by shape)
+constexpr int kPfBN[kPfCfgs] = {PfT32::BN, PfT64::BN, PfT128::BN, PfT256::BN, PfW256::BN, PfW192::BN, PfS64::BN, PfS128::BN};
 constexpr int kCUs = 256;
 
 int g_force_cfg = -1, g_force_splits = 0;
@@ -2766,9 +2771,30 @@ GemmPlan pf_plan(int M, int N, int K) {
   // (128 x 256, four waves, two splits) -> 140. The small projections and
   // down at 128 rows stay on the cost model's choice (the eight-wave tiles
   // measured no better there).
+  // Up to 128 rows, measured per launch with the split reduction (1.5B
+  // shapes, weights from HBM): gate/up on the 64 x 128 eight-wave tile
+  // without a split, 34.2 -> 32.3 us at 128 rows, 29.1 -> 23.5 at 64 and
+  // 26.1 -> 19.7 at 32; where that grid would exceed ~1.25 rounds (the 7B
+  // gate/up, 592 workgroups) the 128 x 256 tile stays ahead.
   if (N >= 8192 && K <= 4096) {
+    if (M <= 128 && (long)((M + 63) / 64) * ((N + 127) / 128) <= 320) {
+      best.cfg = 7;
+      best.splits = 1;
+      return best;
+    }
     best.cfg = 4;
     best.splits = M <= 256 ? std::min(3, K >> 6) : 1;
+    return best;
+  }
+  // Projections up to 2048 wide (qkv, o and down of the 1.5B shape) at up
+  // to 128 rows: the 64 x 64 tile, split so the grid comes to about 240
+  // workgroups. At 128 rows qkv 12.7 -> 11.0 us, o 11.6 -> 10.1, down
+  // 21.9 -> 19.7; at 32-64 rows qkv and o 1.8-3 us faster. The wider 7B
+  // projections measured no better this way and keep the cost model's plan.
+  if (M <= 128 && N <= 2048) {
+    const long tiles = (long)((M + 63) / 64) * ((N + 63) / 64);
+    best.cfg = 6;
+    best.splits = (int)std::max(1L, std::min<long>({(240 + tiles - 1) / tiles, 16L, (long)(K >> 6)}));
     return best;
   }
   if (M > 256 && N <= 4096 && K >= 4096) {
@@ -2869,6 +2895,8 @@ static hipError_t go_pf_cfg(const GemmArgs &a, int cfg, int splits, hipStream_t 
     case 3: return go_pf<PfT256, EPI>(a, splits, s);
     case 4: return go_pf<PfW256, EPI>(a, splits, s);
     case 5: return go_pf<PfW192, EPI>(a, splits, s);
+    case 6: return go_pf<PfS64, EPI>(a, splits, s);
+    case 7: return go_pf<PfS128, EPI>(a, splits, s);
     default: return hipErrorInvalidValue;
   }
 }
