@@ -2410,6 +2410,236 @@ __global__ void __launch_bounds__(256) attn_prefill_merge_kernel(AttnPrefillArgs
   *(uint2 *)(a.out_lo + idx) = make_uint2(lo[0] | ((uint32_t)lo[1] << 16), lo[2] | ((uint32_t)lo[3] << 16));
 }
 
+// Causal prefill attention for short prompts (head_dim 128, at most 128
+// queries, at most 256 keys): workgroup (q head h, 32 queries), wave w takes
+// key blocks w, w + 4, ... of the queries' causal range. A key block is used
+// by one wave only, so its K and V go straight from the cache into MFMA
+// operand registers, with no LDS staging and no barrier per block:
+//   S^T = K Q^T as in attn_prefill_mfma_kernel (lane l holds key l % 32,
+//     dims 16 ks + 8 (l / 32) .. + 7 of the block as the A operand);
+//   O^T += V^T P^T with the lane's own probabilities as the B operand: its
+//     probability j of key step s belongs to key 16 s + 8 (j / 4) +
+//     4 (l / 32) + j % 4, so the A operand holds V[that key][32 n + l % 32]
+//     (each load a 128-byte row segment per half-wave).
+// Each wave keeps an online softmax over its blocks (scores in base 2); the
+// waves' (max, sum, unnormalised o) are merged through LDS in wave order,
+// out = sum_w 2^(m_w - M) o_w / sum_w 2^(m_w - M) l_w, and written as bf16
+// hi / lo planes. One launch, no partials in global memory, and Q is read
+// once per wave: at 128 ids the key-split kernel's four splits each pulled
+// their block's 64 KB of Q and left a merge launch behind them. A wave
+// issues its block's K and V loads together, so the V round trip overlaps
+// the score MFMAs (that alone took the 128-id prefill 2.65 -> 2.59 ms).
+constexpr int kFsQ = 32;
+constexpr int kFsLds = (4 * kFsQ * (kFaD + 4) + 4 * kFsQ * 2) * (int)sizeof(float);
+
+__global__ void __launch_bounds__(256) attn_prefill_small_kernel(AttnPrefillArgs a) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t fs_sm[];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int h = blockIdx.x, g = h / (a.nq / a.nkv);
+  const int q0 = blockIdx.y * kFsQ;
+  const int qi = q0 + (lane & 31);  // this lane's query
+  const bool active = qi < a.M;
+  const int qpos = a.start_pos + (active ? qi : a.M - 1);
+  const int last_pos = a.start_pos + min(a.M - 1, q0 + kFsQ - 1);  // the workgroup's last query
+  const int nball = last_pos / kFaK + 1;
+  const float scale2 = 1.4426950408889634f / sqrtf((float)kFaD);
+  const int qd = a.nq * kFaD;
+
+  // Q^T operand: lane l, step ks -> query l % 32, dims 16 ks + 8 (l / 32) .. + 7
+  bf16x8 qh[8], ql[8];
+  {
+    const float *qrow = a.q + (size_t)(active ? qi : a.M - 1) * qd + h * kFaD + 8 * (lane >> 5);
+#pragma unroll
+    for (int ks = 0; ks < 8; ks++) {
+      const float4 x0 = *(const float4 *)(qrow + 16 * ks), x1 = *(const float4 *)(qrow + 16 * ks + 4);
+      const float v[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        const __bf16 hb = (__bf16)v[e];
+        qh[ks][e] = hb;
+        ql[ks][e] = (__bf16)(v[e] - (float)hb);
+      }
+    }
+  }
+  // 8 consecutive cached values from element offset i (f32 or bf16 cache)
+  auto kv8 = [&](const void *base, size_t i, float *v) {
+    if (a.kv_bf16) {
+      const uint4 w = *(const uint4 *)((const uint16_t *)base + i);
+      const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        v[2 * e] = bf_lo(ww[e]);
+        v[2 * e + 1] = bf_hi(ww[e]);
+      }
+    } else {
+      const float4 x0 = *(const float4 *)((const float *)base + i), x1 = *(const float4 *)((const float *)base + i + 4);
+      v[0] = x0.x, v[1] = x0.y, v[2] = x0.z, v[3] = x0.w, v[4] = x1.x, v[5] = x1.y, v[6] = x1.z, v[7] = x1.w;
+    }
+  };
+  auto kv1 = [&](const void *base, size_t i) {
+    return a.kv_bf16 ? bf16f(((const uint16_t *)base)[i]) : ((const float *)base)[i];
+  };
+  const size_t head_base = (size_t)g * a.max_seq * kFaD;
+
+  f32x16 o[4];
+#pragma unroll
+  for (int n = 0; n < 4; n++)
+#pragma unroll
+    for (int e = 0; e < 16; e++) o[n][e] = 0.f;
+  float mx = -INFINITY, l = 0.f;
+
+  for (int b = wave; b < nball; b += 4) {
+    const int kb = b * kFaK;
+    // K rows past the last query are read at the last query's row (in range;
+    // their scores are masked)
+    const int kpos = min(kb + (lane & 31), last_pos);
+    f32x16 s0, s1, s2;
+#pragma unroll
+    for (int e = 0; e < 16; e++) {
+      s0[e] = 0.f;
+      s1[e] = 0.f;
+      s2[e] = 0.f;
+    }
+    float kv[8][8];
+#pragma unroll
+    for (int ks = 0; ks < 8; ks++) kv8(a.kc, head_base + (size_t)kpos * kFaD + 16 * ks + 8 * (lane >> 5), kv[ks]);
+    // the block's V operand values, loaded with K so that their round trip
+    // overlaps the score MFMAs; keys past the last query read as zero (their
+    // probabilities are zero too)
+    float vv[2][4][8];
+#pragma unroll
+    for (int s2i = 0; s2i < 2; s2i++)
+#pragma unroll
+      for (int n = 0; n < 4; n++)
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+          const int key = kb + 16 * s2i + 8 * (j >> 2) + 4 * (lane >> 5) + (j & 3);
+          const float x = kv1(a.vc, head_base + (size_t)min(key, last_pos) * kFaD + 32 * n + (lane & 31));
+          vv[s2i][n][j] = key <= last_pos ? x : 0.f;
+        }
+#pragma unroll
+    for (int ks = 0; ks < 8; ks++) {
+      bf16x8 kh, kl;
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        const __bf16 hb = (__bf16)kv[ks][e];
+        kh[e] = hb;
+        kl[e] = (__bf16)(kv[ks][e] - (float)hb);
+      }
+      s0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kh, qh[ks], s0, 0, 0, 0);
+      s1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kl, qh[ks], s1, 0, 0, 0);
+      s2 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kh, ql[ks], s2, 0, 0, 0);
+    }
+    float sc[16];
+    float bm = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+      const int key = kb + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
+      sc[i] = key <= qpos ? ((s0[i] + s1[i]) + s2[i]) * scale2 : -INFINITY;
+      bm = fmaxf(bm, sc[i]);
+    }
+    bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
+    const float mnew = fmaxf(mx, bm);
+    float p[16];
+    if (mnew != -INFINITY) {
+      const float corr = __builtin_amdgcn_exp2f(mx - mnew);  // mx = -inf: 0
+      float ps = 0.f;
+#pragma unroll
+      for (int i = 0; i < 16; i++) {
+        p[i] = __builtin_amdgcn_exp2f(sc[i] - mnew);  // masked: 2^-inf = 0
+        ps += p[i];
+      }
+      ps += __shfl_xor(ps, 32, 64);
+      l = l * corr + ps;
+      mx = mnew;
+#pragma unroll
+      for (int n = 0; n < 4; n++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) o[n][e] *= corr;
+    } else {
+#pragma unroll
+      for (int i = 0; i < 16; i++) p[i] = 0.f;
+    }
+#pragma unroll
+    for (int s2i = 0; s2i < 2; s2i++) {
+      bf16x8 ph, pl;
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        const float v = p[8 * s2i + e];
+        const __bf16 hb = (__bf16)v;
+        ph[e] = hb;
+        pl[e] = (__bf16)(v - (float)hb);
+      }
+#pragma unroll
+      for (int n = 0; n < 4; n++) {
+        bf16x8 vah, val;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+          const float x = vv[s2i][n][j];
+          const __bf16 hb = (__bf16)x;
+          vah[j] = hb;
+          val[j] = (__bf16)(x - (float)hb);
+        }
+        o[n] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vah, ph, o[n], 0, 0, 0);
+        o[n] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(val, ph, o[n], 0, 0, 0);
+        o[n] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vah, pl, o[n], 0, 0, 0);
+      }
+    }
+  }
+
+  // merge the waves: o^T tile n, lane l holds dims 32 n + 8 (i / 4) +
+  // 4 (l / 32) + i % 4 of query l % 32
+  float *om = (float *)fs_sm;                  // [wave][query][kFaD + 4]
+  float *mlp = om + 4 * kFsQ * (kFaD + 4);     // [wave][query][2]
+#pragma unroll
+  for (int n = 0; n < 4; n++)
+#pragma unroll
+    for (int i = 0; i < 16; i++)
+      om[(wave * kFsQ + (lane & 31)) * (kFaD + 4) + 32 * n + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3)] = o[n][i];
+  if (lane < 32) {
+    mlp[(wave * kFsQ + lane) * 2] = mx;
+    mlp[(wave * kFsQ + lane) * 2 + 1] = l;
+  }
+  __syncthreads();
+  // thread t: query t / 8, dims 16 (t % 8) .. + 15
+  const int qq = tid >> 3, d0 = (tid & 7) * 16;
+  float mw[4], lw[4], mall = -INFINITY;
+#pragma unroll
+  for (int w = 0; w < 4; w++) {
+    mw[w] = mlp[(w * kFsQ + qq) * 2];
+    lw[w] = mlp[(w * kFsQ + qq) * 2 + 1];
+    mall = fmaxf(mall, mw[w]);
+  }
+  float ew[4], lsum = 0.f;
+#pragma unroll
+  for (int w = 0; w < 4; w++) {
+    ew[w] = mw[w] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mw[w] - mall);
+    lsum = fmaf(ew[w], lw[w], lsum);
+  }
+  const float inv = 1.0f / lsum;
+  const int qrow = q0 + qq;
+  if (qrow < a.M) {
+#pragma unroll
+    for (int half = 0; half < 2; half++) {
+      bf16x8 hi, lo;
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        const int d = d0 + 8 * half + e;
+        float acc = 0.f;
+#pragma unroll
+        for (int w = 0; w < 4; w++) acc = fmaf(ew[w], om[(w * kFsQ + qq) * (kFaD + 4) + d], acc);
+        const float v = acc * inv;
+        const __bf16 hb = (__bf16)v;
+        hi[e] = hb;
+        lo[e] = (__bf16)(v - (float)hb);
+      }
+      const size_t idx = (size_t)qrow * qd + h * kFaD + d0 + 8 * half;
+      *(bf16x8 *)(a.out_hi + idx) = hi;
+      *(bf16x8 *)(a.out_lo + idx) = lo;
+    }
+  }
+}
+
 inline unsigned nblk(size_t n, unsigned b) { return (unsigned)((n + b - 1) / b); }
 constexpr long kCUsGemv = 256;
 
@@ -2978,6 +3208,23 @@ hipError_t launch_attn_prefill(const AttnPrefillArgs &a, hipStream_t s) {
   // the MFMA kernel's buffer loads address the layer's cache with 32-bit
   // offsets and use 2^31 as the out-of-range offset
   const size_t kv_bytes = (size_t)a.nkv * a.max_seq * a.head_dim * (a.kv_bf16 ? 2 : 4);
+  if (a.head_dim == kFaD && a.nq % a.nkv == 0 && a.M > kFsQ && a.M <= 128 && a.start_pos + a.M <= 256) {
+    // short prompts: one launch, a key block per wave. Measured per prefill
+    // (1.5B shape, same box): 128 ids 2.70 -> 2.59 ms, 64 ids 2.19 -> 2.13;
+    // at 32 ids or fewer a single wave would carry all the keys, and the
+    // key-split kernel, whose four waves stage each block together, stays
+    // ahead (1.86 against 1.88 ms)
+    static bool small_attr = false;
+    const void *fn = (const void *)attn_prefill_small_kernel;
+    if (!small_attr) {
+      hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, kFsLds);
+      if (e != hipSuccess) return e;
+      small_attr = true;
+    }
+    AttnPrefillArgs args = a;
+    void *params[] = {&args};
+    return hipLaunchKernel(fn, dim3(a.nq, (unsigned)nblk((size_t)a.M, kFsQ)), dim3(256), params, kFsLds, s);
+  }
   if (a.head_dim == kFaD && a.nq % a.nkv == 0 && kv_bytes < (size_t(1) << 31)) {
     static bool attr_done = false;
     const void *fn = (const void *)attn_prefill_mfma_kernel;

@@ -279,6 +279,39 @@ def test_prefill_attention_key_groups(tmp_path, dims, m):
     g.close()
 
 
+# Short prompts with head_dim 128 (33 to 128 ids, at most 256 keys) take the
+# one-launch kernel that gives each wave its own key blocks; a prefill in
+# chunks reaches it with a cache already holding rows (start position > 0),
+# up to the 256-key limit. Each chunk's last logits and the final cache
+# rows against the oracle's prefill of the same chunks.
+@pytest.mark.parametrize("kv", [myos.KV_F32, myos.KV_BF16], ids=["f32_kv", "bf16_kv"])
+@pytest.mark.parametrize("chunks", [(33,), (50, 70), (128, 128), (20, 100, 36)])
+def test_short_prompt_attention_in_chunks(tmp_path, kv, chunks):
+    s = shape_dict(512, 4, 1, 128, 1536, 2048, 2, 1e-6)
+    t = random_map(s, seed=sum(chunks) + 11, std=0.05)
+    n = sum(chunks)
+    g, o = open_pair(tmp_path, s, t, n + 4, kv=kv)
+    ids = np.random.default_rng(n).integers(0, s["vocab"], n)
+    tol = 1e-4 if kv == myos.KV_F32 else 2e-3
+    at = 0
+    for c in chunks:
+        g.prefill(ids[at:at + c])
+        assert o.prefill(ids[at:at + c]) == 0
+        at += c
+        assert g.cache_len() == at
+        assert max_rel(g.logits(), o.logits()) < tol, (chunks, at)
+        assert max_rel(g.hidden(), o.hidden()) < tol, (chunks, at)
+    # layer-1 cache rows: with a bf16 cache a row value a few f32 ulps from
+    # the oracle's may round to the neighbouring bf16 value, one bf16 ulp
+    # (2^-7 of the row's largest value at most)
+    kv_tol = tol if kv == myos.KV_F32 else 2.0 ** -7
+    for pos in (0, n // 2, n - 1):
+        k, v = g.kv(1, 0, pos)
+        ok, ov = o.kv(1, 0, pos)
+        assert max_rel(k, ok) <= kv_tol and max_rel(v, ov) <= kv_tol, pos
+    g.close()
+
+
 # -------------------------------------------------- Qwen2.5-1.5B shape ----
 
 @pytest.fixture(scope="module")
