@@ -2969,9 +2969,14 @@ using PfW192 = PfCfg<1, 3, 4, 2>;
 // narrow projections, 64 x 128 with eight waves for gate/up.
 using PfS64 = PfCfg<1, 1, 2, 2>;
 using PfS128 = PfCfg<1, 1, 2, 4>;
-constexpr int kPfCfgs = 8;
+// 64 x 160 with ten waves: a 17920-row gate/up at 65-128 rows is 224
+// workgroups, one round over the CUs, where the 64 x 128 tile's 280 put two
+// workgroups on 24 CUs
+using PfS160 = PfCfg<1, 1, 2, 5>;
+constexpr int kPfCfgs = 9;
 constexpr int kPfPlanCfgs = 4;  // the cost model's candidates (the others are picked by shape)
-constexpr int kPfBN[kPfCfgs] = {PfT32::BN, PfT64::BN, PfT128::BN, PfT256::BN, PfW256::BN, PfW192::BN, PfS64::BN, PfS128::BN};
+constexpr int kPfBN[kPfCfgs] = {PfT32::BN, PfT64::BN, PfT128::BN, PfT256::BN, PfW256::BN, PfW192::BN, PfS64::BN, PfS128::BN,
+                                PfS160::BN};
 constexpr int kCUs = 256;
 
 int g_force_cfg = -1, g_force_splits = 0;
@@ -3002,12 +3007,19 @@ GemmPlan pf_plan(int M, int N, int K) {
   // down at 128 rows stay on the cost model's choice (the eight-wave tiles
   // measured no better there).
   // Up to 128 rows, measured per launch with the split reduction (1.5B
-  // shapes, weights from HBM): gate/up on the 64 x 128 eight-wave tile
-  // without a split, 34.2 -> 32.3 us at 128 rows, 29.1 -> 23.5 at 64 and
-  // 26.1 -> 19.7 at 32; where that grid would exceed ~1.25 rounds (the 7B
+  // shapes, weights from HBM): gate/up without a split on the 64 x 160
+  // ten-wave tile where its grid fits one round (34.2 -> 26.7 us at 128
+  // rows), else on the 64 x 128 eight-wave tile (29.1 -> 23.5 us at 64 rows,
+  // 26.1 -> 19.7 at 32); where that grid would exceed ~1.25 rounds (the 7B
   // gate/up, 592 workgroups) the 128 x 256 tile stays ahead.
   if (N >= 8192 && K <= 4096) {
-    if (M <= 128 && (long)((M + 63) / 64) * ((N + 127) / 128) <= 320) {
+    const long mt64 = (M + 63) / 64;
+    if (M > 64 && M <= 128 && mt64 * ((N + 159) / 160) <= kCUs) {
+      best.cfg = 8;
+      best.splits = 1;
+      return best;
+    }
+    if (M <= 128 && mt64 * ((N + 127) / 128) <= 320) {
       best.cfg = 7;
       best.splits = 1;
       return best;
@@ -3127,6 +3139,7 @@ static hipError_t go_pf_cfg(const GemmArgs &a, int cfg, int splits, hipStream_t 
     case 5: return go_pf<PfW192, EPI>(a, splits, s);
     case 6: return go_pf<PfS64, EPI>(a, splits, s);
     case 7: return go_pf<PfS128, EPI>(a, splits, s);
+    case 8: return go_pf<PfS160, EPI>(a, splits, s);
     default: return hipErrorInvalidValue;
   }
 }
