@@ -2973,10 +2973,14 @@ using PfS128 = PfCfg<1, 1, 2, 4>;
 // workgroups, one round over the CUs, where the 64 x 128 tile's 280 put two
 // workgroups on 24 CUs
 using PfS160 = PfCfg<1, 1, 2, 5>;
-constexpr int kPfCfgs = 9;
+// 128 x 128 with eight waves (32 x 64 each): over 256 rows it takes the
+// 128 x 128 plans of the cost model (qkv 40.0 -> 32.4 us, o 38.0 -> 29.9 at
+// 2048 rows of the 1.5B shape)
+using PfW128 = PfCfg<1, 2, 4, 2>;
+constexpr int kPfCfgs = 10;
 constexpr int kPfPlanCfgs = 4;  // the cost model's candidates (the others are picked by shape)
 constexpr int kPfBN[kPfCfgs] = {PfT32::BN, PfT64::BN, PfT128::BN, PfT256::BN, PfW256::BN, PfW192::BN, PfS64::BN, PfS128::BN,
-                                PfS160::BN};
+                                PfS160::BN, PfW128::BN};
 constexpr int kCUs = 256;
 
 int g_force_cfg = -1, g_force_splits = 0;
@@ -3066,6 +3070,7 @@ GemmPlan pf_plan(int M, int N, int K) {
       }
     }
   }
+  if (M > 256 && best.cfg == 2) best.cfg = 9;  // the eight-wave 128 x 128 tile
   return best;
 }
 
@@ -3140,6 +3145,7 @@ static hipError_t go_pf_cfg(const GemmArgs &a, int cfg, int splits, hipStream_t 
     case 6: return go_pf<PfS64, EPI>(a, splits, s);
     case 7: return go_pf<PfS128, EPI>(a, splits, s);
     case 8: return go_pf<PfS160, EPI>(a, splits, s);
+    case 9: return go_pf<PfW128, EPI>(a, splits, s);
     default: return hipErrorInvalidValue;
   }
 }
