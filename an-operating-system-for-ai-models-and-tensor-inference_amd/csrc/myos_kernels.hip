@@ -3028,19 +3028,35 @@ GemmPlan pf_plan(int M, int N, int K) {
       best.splits = 1;
       return best;
     }
+    // (the 7B gate/up at 128 rows: 110.8 us with three splits, 107.5 with none)
     best.cfg = 4;
-    best.splits = M <= 256 ? std::min(3, K >> 6) : 1;
+    best.splits = M > 128 && M <= 256 ? std::min(3, K >> 6) : 1;
     return best;
   }
-  // Projections up to 2048 wide (qkv, o and down of the 1.5B shape) at up
-  // to 128 rows: the 64 x 64 tile, split so the grid comes to about 240
-  // workgroups. At 128 rows qkv 12.7 -> 11.0 us, o 11.6 -> 10.1, down
-  // 21.9 -> 19.7; at 32-64 rows qkv and o 1.8-3 us faster. The wider 7B
-  // projections measured no better this way and keep the cost model's plan.
-  if (M <= 128 && N <= 2048) {
-    const long tiles = (long)((M + 63) / 64) * ((N + 63) / 64);
-    best.cfg = 6;
-    best.splits = (int)std::max(1L, std::min<long>({(240 + tiles - 1) / tiles, 16L, (long)(K >> 6)}));
+  // The other projections at up to 128 rows, except long-K ones wider than
+  // 2048 (the 7B down keeps the cost model's plan): a 64-row tile split so
+  // the grid fills one round over the CUs, the 64 x 64 four-wave tile or the
+  // 64 x 128 eight-wave one, whichever comes closer to 256 workgroups (the
+  // 64 x 64 on a tie). At 128 rows qkv 12.7 -> 11.0 us, o 11.6 -> 10.1,
+  // down 21.9 -> 19.7 (1.5B); 7B qkv 26.3 -> 22.6 (64 x 128, 3 splits), 7B
+  // o 21.5 -> 19.6 (64 x 64, 2 splits); at 32-64 rows qkv and o 1.8-3 us
+  // faster.
+  if (M <= 128 && (N <= 2048 || K <= 4096)) {
+    const long mt64 = (M + 63) / 64;
+    auto fill = [&](int bn, int *sp) {
+      const long tiles = mt64 * ((N + bn - 1) / bn);
+      *sp = (int)std::max(1L, std::min<long>({kCUs / tiles, 16L, (long)(K >> 6)}));
+      return tiles * *sp;
+    };
+    int s64 = 1, s128 = 1;
+    const long w64 = fill(64, &s64), w128 = fill(128, &s128);
+    if (w128 > w64 && w128 <= kCUs) {
+      best.cfg = 7;
+      best.splits = s128;
+    } else {
+      best.cfg = 6;
+      best.splits = s64;
+    }
     return best;
   }
   if (M > 256 && N <= 4096 && K >= 4096) {
