@@ -85,16 +85,21 @@ def test_gemv_order_cancellation():
     assert np.all(np.isin(got, [0.0, 1.0, 2.0, 3.0, 4.0]))
 
 
-# the planner's tile shapes: 128 x 32 split K (128, 1536, 1536), 128 x 64
-# split K (128, 1536, 8960), 128 x 64 over several row tiles with tails
-# (1100, 1536, 640), 128 x 128 (600, 4096, 512), 128 x 256 (1100, 4096, 256);
-# the eight-wave 128 x 256 tile for wide short-K shapes, split with a row tail
-# (37, 8960, 1536) and unsplit over row tiles with a tail (300, 8960, 512),
-# and for long K over many rows in two splits (300, 1280, 4096); the
+# every tile the planner picks (pf_plan), with the split counts and row
+# tails it gives these shapes: 64 x 64 split K (128, 1536, 1536) in 5,
+# (128, 256, 1536) in 16 and (128, 1536, 8960) in 5 splits; the eight-wave
+# 64 x 128 tile unsplit with a row tail (37, 8960, 1536) and in 3 splits
+# (128, 4608, 3584); the ten-wave 64 x 160 tile over two row tiles with a tail
+# (100, 17920, 1536); 128 x 64 over several row tiles with tails
+# (1100, 1536, 640); 128 x 128 in 10 splits with a row tail (200, 1536, 8960);
+# the eight-wave 128 x 128 tile (600, 4096, 512); 128 x 256 (1100, 4096, 256);
+# the eight-wave 128 x 256 tile unsplit over row tiles with a tail
+# (300, 8960, 512) and for long K in two splits (300, 1280, 4096); the
 # eight-wave 128 x 192 tile for long K when N % 192 == 0, two splits with a
 # row tail (300, 1536, 4096); the single-stage kernel for K % 64 != 0
 @pytest.mark.parametrize("batch,m,k", [(128, 1536, 1536), (128, 256, 1536), (37, 8960, 1536),
-                                       (128, 1536, 8960), (1100, 1536, 640), (1100, 4096, 256),
+                                       (128, 1536, 8960), (128, 4608, 3584), (100, 17920, 1536),
+                                       (1100, 1536, 640), (200, 1536, 8960), (1100, 4096, 256),
                                        (600, 4096, 512), (300, 8960, 512), (300, 1536, 4096),
                                        (300, 1280, 4096),
                                        (5, 7, 3), (33, 70, 45), (200, 130, 200)])
