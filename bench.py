@@ -15,6 +15,9 @@ model's stream), the parity of the timed run against the oracle, the
 fresh-process W/R medians of the CLI's arena harness, and the CPU oracle on
 the same workload (medians, host core count and 8 threads). The host-only
 legs (oracle, arena children) run before this process touches the GPU.
+After the timed region, each on its own model: a 2048-id prefill alone, the
+long-context workload (2048 ids + 256 greedy steps, bf16 cache) and the
+7B shape's S1 (128 + 128).
 """
 from __future__ import annotations
 
@@ -93,6 +96,40 @@ def prefill_leg(path, shape, kv, n, reps=3):
     return {"prompt_ids": n, "device_ms": round(t, 3), "tok_s": round(n / (t * 1e-3), 1),
             "flops_alg": fl, "mfma_frac_alg": round(fl / (t * 1e-3) / MFMA_BF16_PEAK, 4),
             "runs": [round(x, 3) for x in ms]}
+
+
+def decode_leg(path, shape, kv, n_prompt, n_decode, is7b, reps=3):
+    """Another workload on its own model, outside the timed region: n_prompt
+    seeded ids prefilled, then n_decode greedy steps on the default decode
+    path; one warm-up, the median device times of reps runs and the decode
+    roofline at each step's cache length."""
+    prompt = bench_prompt(shape, n_prompt)
+    skv = 2 if kv == myos.KV_BF16 else 4
+    pre, dec, ids = [], [], None
+    with myos.Model.open(path, shape, kv, n_prompt + n_decode) as g:
+        pname = {myos.DECODE_PERSISTENT: "persistent", myos.DECODE_STREAMED: "streamed",
+                 myos.DECODE_KERNELS: "kernels"}[g.decode_path()]
+        for r in range(reps + 1):
+            g.cache_clear()
+            g.prefill(prompt)
+            out = g.greedy_decode(n_decode)
+            if r:
+                pre.append(g.last_prefill_ms())
+                dec.append(g.last_decode_ms())
+                ids = ids or out
+    d = float(np.median(dec))
+    seqs = np.arange(n_prompt + 1, n_prompt + n_decode + 1)
+    b_tok = weight_bytes(shape) + float(np.mean([kv_bytes_per_token(shape, int(q), skv) for q in seqs]))
+    tok_s = n_decode / (d * 1e-3)
+    import hashlib
+    return {"workload": workload_name(is7b, n_prompt, n_decode, "bf16" if skv == 2 else "f32"),
+            "decode_path": pname, "decode_tok_s": round(tok_s, 2),
+            "device_ms": {"prefill": round(float(np.median(pre)), 3), "decode": round(d, 3)},
+            "decode_roofline": {"bytes_per_token": int(b_tok),
+                                "achieved_GBps": round(tok_s * b_tok / 1e9, 1),
+                                "frac": round(tok_s * b_tok / HBM_PEAK, 4)},
+            "runs_decode_ms": [round(x, 3) for x in dec],
+            "ids_sha1": hashlib.sha1(np.asarray(ids, np.uint32).tobytes()).hexdigest()[:16]}
 
 
 def gemv_microbench(reps=5):
@@ -232,6 +269,16 @@ def bench_prompt(shape, n):
     return np.random.default_rng(2024).integers(0, shape.vocab, n).astype(np.uint32)
 
 
+PATH_7B = "/tmp/myos_bench/qwen25_7b_seed0.safetensors"
+
+
+def other_legs(args, is7b):
+    """The default S1 run also measures the long-context workload (2048 + 256,
+    bf16 cache) and the 7B shape's S1, each on its own model after the timed
+    region."""
+    return not is7b and args.prompt == 128 and args.decode == 128 and args.kv == "f32"
+
+
 def host_legs(args, is7b, path, n_cpu):
     """The child process of the host-only legs: writes the weights file if it
     is missing, then runs the CPU baseline and the arena; results go to
@@ -243,6 +290,12 @@ def host_legs(args, is7b, path, n_cpu):
         t0 = time.perf_counter()
         myos.write_random_qwen25(path, shape, seed=0, std=0.02, threads=host_cores())
         log(f"weights written in {time.perf_counter() - t0:.1f}s")
+    if other_legs(args, is7b) and not args.no_7b and not os.path.exists(PATH_7B):
+        log(f"writing random-init 7B-shape weights to {PATH_7B}")
+        t0 = time.perf_counter()
+        myos.write_random_qwen25(PATH_7B, myos.preset(myos.SHAPE_QWEN25_7B), seed=0, std=0.02,
+                                 threads=host_cores())
+        log(f"7B weights written in {time.perf_counter() - t0:.1f}s")
     prompt = bench_prompt(shape, args.prompt)
     cpu_res, ref = None, None
     if not args.no_cpu_baseline:
@@ -280,6 +333,9 @@ def main():
     ap.add_argument("--no-gemv-microbench", action="store_true")
     ap.add_argument("--no-prefill-2048", action="store_true",
                     help="skip the 2048-id prefill-only leg")
+    ap.add_argument("--no-long-context", action="store_true",
+                    help="skip the 2048 + 256 bf16-cache decode leg")
+    ap.add_argument("--no-7b", action="store_true", help="skip the 7B-shape S1 decode leg")
     ap.add_argument("--shape", choices=["qwen2.5-1.5b", "qwen2.5-7b"], default="qwen2.5-1.5b",
                     help="model shape (the headline metric is quoted on qwen2.5-1.5b)")
     ap.add_argument("--host-legs", metavar="DIR", help=argparse.SUPPRESS)
@@ -290,8 +346,7 @@ def main():
         sys.exit(2)
 
     is7b = args.shape == "qwen2.5-7b"
-    path = args.weights or ("/tmp/myos_bench/qwen25_7b_seed0.safetensors" if is7b
-                            else "/tmp/myos_bench/qwen25_1_5b_seed0.safetensors")
+    path = args.weights or (PATH_7B if is7b else "/tmp/myos_bench/qwen25_1_5b_seed0.safetensors")
     n_cpu = args.cpu_decode_steps or args.decode
     if args.host_legs:
         host_legs(args, is7b, path, n_cpu)
@@ -463,6 +518,17 @@ def main():
         log(f"prefill 2048 ids: {pf_long['device_ms']} ms ({pf_long['tok_s']} tok/s, "
             f"{pf_long['mfma_frac_alg']} of the bf16 MFMA peak counted algorithmically)")
 
+    legs = {}
+    if other_legs(args, is7b):
+        if not args.no_long_context:
+            legs["long_context"] = decode_leg(path, shape, myos.KV_BF16, 2048, 256, False)
+        if not args.no_7b:
+            legs["qwen25_7b_s1"] = decode_leg(PATH_7B, myos.preset(myos.SHAPE_QWEN25_7B),
+                                              myos.KV_F32, 128, 128, True)
+        for k, v in legs.items():
+            log(f"{k}: {v['decode_tok_s']} tok/s ({v['decode_roofline']['frac']} of the HBM "
+                f"roofline), device ms {v['device_ms']}, {v['decode_path']} path")
+
     micro = None if args.no_gemv_microbench else gemv_microbench()
     if micro:
         log("gemv microbench: " + ", ".join(f"{n} {v['avg_us']}us {v['GBps']}GB/s"
@@ -512,7 +578,8 @@ def main():
                             "frac": round(decode_frac, 4)},
         "prefill_roofline": pf_roof,
         "roofline": roofline, "parity": parity, "arena": arena,
-        "per_kernel_path": kernels, "prefill_2048": pf_long, "gemv_microbench": micro,
+        "per_kernel_path": kernels, "prefill_2048": pf_long, "other_workloads": legs or None,
+        "gemv_microbench": micro,
         "t_load_s": round(t_load, 2),
         "cpu_baseline": cpu,
     }
