@@ -98,6 +98,21 @@ def prefill_leg(path, shape, kv, n, reps=3):
             "runs": [round(x, 3) for x in ms]}
 
 
+def committed_traffic(is7b, path_name, n_prompt, n_decode, kv_name):
+    """The committed rocprof HBM traffic of one cooperative decode launch of
+    this workload (profiles/decode_traffic_*.json, FETCH_SIZE + WRITE_SIZE
+    scaled by a copy-kernel calibration), or (None, None)."""
+    tpath = os.path.join(ROOT, "profiles", f"decode_traffic_qwen25_{'7b' if is7b else '1_5b'}.json")
+    if not os.path.exists(tpath):
+        return None, None
+    for key, t in json.load(open(tpath)).items():
+        if (key.startswith(f"{path_name}_launch") and isinstance(t, dict)
+                and t.get("prompt_ids") == n_prompt and t.get("decode_steps") == n_decode
+                and t.get("kv_cache", "f32") == kv_name):
+            return t["traffic_bytes"], t["source"]
+    return None, None
+
+
 def decode_leg(path, shape, kv, n_prompt, n_decode, is7b, reps=3):
     """Another workload on its own model, outside the timed region: n_prompt
     seeded ids prefilled, then n_decode greedy steps on the default decode
@@ -121,13 +136,17 @@ def decode_leg(path, shape, kv, n_prompt, n_decode, is7b, reps=3):
     seqs = np.arange(n_prompt + 1, n_prompt + n_decode + 1)
     b_tok = weight_bytes(shape) + float(np.mean([kv_bytes_per_token(shape, int(q), skv) for q in seqs]))
     tok_s = n_decode / (d * 1e-3)
+    kv_name = "bf16" if skv == 2 else "f32"
+    traffic, tsrc = committed_traffic(is7b, pname, n_prompt, n_decode, kv_name)
     import hashlib
-    return {"workload": workload_name(is7b, n_prompt, n_decode, "bf16" if skv == 2 else "f32"),
+    return {"workload": workload_name(is7b, n_prompt, n_decode, kv_name),
             "decode_path": pname, "decode_tok_s": round(tok_s, 2),
             "device_ms": {"prefill": round(float(np.median(pre)), 3), "decode": round(d, 3)},
             "decode_roofline": {"bytes_per_token": int(b_tok),
                                 "achieved_GBps": round(tok_s * b_tok / 1e9, 1),
-                                "frac": round(tok_s * b_tok / HBM_PEAK, 4)},
+                                "frac": round(tok_s * b_tok / HBM_PEAK, 4),
+                                "launch_traffic": traffic, "launch_algorithmic_bytes": int(b_tok * n_decode),
+                                "traffic_source": tsrc and f"{tsrc} (not measured in this run)"},
             "runs_decode_ms": [round(x, 3) for x in dec],
             "ids_sha1": hashlib.sha1(np.asarray(ids, np.uint32).tobytes()).hexdigest()[:16]}
 
@@ -480,16 +499,13 @@ def main():
                                         for n, v in kernels.items()))
     tpath = os.path.join(ROOT, "profiles",
                          f"decode_traffic_qwen25_{'7b' if is7b else '1_5b'}.json")
-    # the committed traffic figures are for the f32 cache
+    # the committed per-kernel traffic figures are for the f32 cache
     tinfo = json.load(open(tpath)) if os.path.exists(tpath) and kv == myos.KV_F32 else {}
     if path_name in ("persistent", "streamed"):
         launch_bytes = b_tok * args.decode
         launch_s = dd / args.steps * 1e-3
         achieved = launch_bytes / launch_s
-        traffic, tsrc = None, None
-        t = tinfo.get(f"{path_name}_launch")
-        if t and t.get("decode_steps") == args.decode and t.get("prompt_ids") == args.prompt:
-            traffic, tsrc = t["traffic_bytes"], t["source"]
+        traffic, tsrc = committed_traffic(is7b, path_name, args.prompt, args.decode, args.kv)
         roofline = {"bound": "hbm",
                     "kernel": f"{'decode_persistent_kernel' if path_name == 'persistent' else 'decode_wide_kernel'} "
                               f"(one launch: {args.decode} greedy decode steps)",
