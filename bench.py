@@ -36,7 +36,7 @@ myos = importlib.import_module("an-operating-system-for-ai-models-and-tensor-inf
 
 HBM_PEAK = 8.0e12  # MI355X HBM3E, bytes/s
 MFMA_BF16_PEAK = 2.5e15  # MI355X dense bf16 MFMA, FLOP/s
-REF_CPU_DECODE_TOK_S = 15.4880  # reference S1 decode tok/s, 8 threads
+REF_CPU_DECODE_TOK_S = 15.4880  # reference S1 decode tok/s, 8 threads (arena/phase1-scoreboard.md:28)
 METRIC = "decode tok/s + % HBM roofline, Qwen2.5-1.5B-shape bf16 bs=1; prefill tok/s"
 
 
@@ -53,7 +53,7 @@ def host_nproc() -> int:
 
 def host_cores() -> int:
     # the reference caps --threads at 64 (gemv_bf16_kernel.rs:34,
-    # main.rs:416-424); a GPU box allots 16 host cores per GPU
+    # main.rs:416-424); the benchmark hosts allot 16 host cores per GPU
     return max(1, min(16, host_nproc(), 64))
 
 
@@ -559,8 +559,8 @@ def main():
                "sample": f"same weights file and {args.prompt} prompt ids: prefill then {n_cpu} "
                          f"greedy decode steps on the C oracle (AVX2 32-row GEMV over a "
                          f"row-span thread pool), median of {args.cpu_repeats} runs after a "
-                         f"warm-up, at {cores} threads (host nproc {host_nproc()}; a GPU box "
-                         f"allots 16 cores per GPU) and at 8 threads",
+                         f"warm-up, at {cores} threads (host nproc {host_nproc()}; the benchmark "
+                         f"hosts allot 16 cores per GPU) and at 8 threads",
                "host_nproc": host_nproc(),
                "prefill_tok_s": round(len(prompt) / r["prefill_s"], 2),
                "threads8_decode_tok_s": round(n_cpu / cpu_res[8]["decode_s"], 3) if 8 in cpu_res else None,
