@@ -631,7 +631,9 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
   // issued before them, so loads go out right after a wait returns and drain
   // while the next phase computes, each batch as soon as its registers are
   // free:
-  //   after the items of l (before the merge): gate/up slots 1-4 of l
+  //   after the items of l (before the merge): gate/up slots 1-4 of l (with
+  //                                            head attention slots 1-3, and
+  //                                            slot 4 after the X_o wait)
   //   during gate/up(l), after slot 0's dots:  gate/up slot 0 of l+1
   //   after the down partials of l:            QKV(l+1), o(l+1)
   // A wave that issues more loads than its memory queue holds stalls at the
@@ -1335,14 +1337,16 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
         }
       }
 
-      // with head attention the attention-output wait comes right after QKV,
-      // so the last gate/up slot waits until after it
-      if (HA) issue_gu(l, true, 4);
       issue_wdp(l, 2);
       // ---- gate/up + SwiGLU + down partials (tag T + P_PD) ----------------------
       load_gw<HC>(gw, Lln2, H, lane);
       tgather_lin<3>(a.txo, H, T + P_XO, xs, a, &fail_s);
       mark(a, s, 4 + 5 * l);
+      // With head attention the attention-output wait comes right after QKV,
+      // so the last gate/up slot is not issued with slots 1-3; issued before
+      // the X_o wait it held that wait 1.3 us, so it goes out after it, and
+      // its dots come last: the first four slots' dots cover its round trip.
+      if (HA) issue_gu(l, true, 4);
       // every dot first, then the stores
       float gy[GPMAX][2];
       {
