@@ -4,6 +4,7 @@ closed forms of the workloads (1.5B: 28 layers of 46,797,824 bf16 weights,
 the final norm, the tied 151936 x 1536 head and one embedding row per token;
 KV 28 x 2 x 2 x 128 values per position)."""
 import importlib.util
+import json
 import os
 
 import pytest
@@ -57,13 +58,39 @@ def test_workload_names(bench):
     assert "S1" not in bench.workload_name(False, 64, 32, "f32")
 
 
+def _entries(name):
+    with open(os.path.join(ROOT, "profiles", name)) as f:
+        return {k: v for k, v in json.load(f).items() if isinstance(v, dict) and "fetch_kib" in v}
+
+
+def test_committed_traffic_is_the_scaled_counters():
+    # traffic = FETCH_SIZE KiB x 1024 x fetch factor + WRITE_SIZE KiB x 1024 x
+    # write factor; the stored figure was summed from unrounded per-dispatch
+    # counters, the KiB means and factors are printed to 0.1 KiB / 1e-6
+    n = 0
+    for name in ("decode_traffic_qwen25_1_5b.json", "decode_traffic_qwen25_7b.json"):
+        for key, e in _entries(name).items():
+            scaled = e["fetch_kib"] * 1024 * e["fetch_factor"] + e["write_kib"] * 1024 * e["write_factor"]
+            assert e["traffic_bytes"] == pytest.approx(scaled, rel=2e-6), key
+            assert 1.0 < e["fetch_factor"] < 2.5 and e["write_factor"] == pytest.approx(1.0, abs=0.05)
+            n += 1
+    assert n >= 3
+
+
 def test_committed_traffic_lookup(bench):
+    e15 = _entries("decode_traffic_qwen25_1_5b.json")
+    e7 = _entries("decode_traffic_qwen25_7b.json")
     t, src = bench.committed_traffic(False, "persistent", 128, 128, "f32")
-    assert t == 420_203_750_485 and src.endswith("decode_persistent_qwen25_1_5b_s1.md")
+    assert t == e15["persistent_launch"]["traffic_bytes"]
+    assert src.endswith("decode_persistent_qwen25_1_5b_s1.md")
+    # the S1 launch moves at least its algorithmic bytes and at most 1.2x them
+    assert 396_604_211_200 < t < 1.2 * 396_604_211_200
     t, src = bench.committed_traffic(False, "persistent", 2048, 256, "bf16")
-    assert t == 872_807_582_937 and src.endswith("decode_persistent_qwen25_1_5b_long_bf16.md")
+    assert t == e15["persistent_launch_long_bf16"]["traffic_bytes"]
+    assert src.endswith("decode_persistent_qwen25_1_5b_long_bf16.md")
+    assert 806_358_089_728 < t < 1.2 * 806_358_089_728
     t, _ = bench.committed_traffic(True, "streamed", 128, 128, "f32")
-    assert t == 1_811_771_947_376
+    assert t == e7["streamed_launch"]["traffic_bytes"]
     # no figure for a workload that was not profiled, or for another cache dtype
     assert bench.committed_traffic(False, "persistent", 2048, 256, "f32") == (None, None)
     assert bench.committed_traffic(False, "persistent", 64, 8, "f32") == (None, None)
