@@ -631,9 +631,8 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
   // issued before them, so loads go out right after a wait returns and drain
   // while the next phase computes, each batch as soon as its registers are
   // free:
-  //   after the items of l (before the merge): gate/up slots 1-4 of l (with
-  //                                            head attention slots 1-3, and
-  //                                            slot 4 after the X_o wait)
+  //   after the items of l (before the merge): gate/up slots 1-3 of l
+  //   after the X_o wait of l:                 gate/up slot 4 of l
   //   during gate/up(l), after slot 0's dots:  gate/up slot 0 of l+1
   //   after the down partials of l:            QKV(l+1), o(l+1)
   // A wave that issues more loads than its memory queue holds stalls at the
@@ -1280,7 +1279,6 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
       issue_gu(l, true, 1);
       issue_gu(l, true, 2);
       issue_gu(l, true, 3);
-      if (!HA) issue_gu(l, true, 4);
 
       // ---- merge: q head h's chunks -> att[h] (tag T + P_ATT), on the last
       // workgroups (attention items start at the first); one wave combines
@@ -1342,11 +1340,11 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
       load_gw<HC>(gw, Lln2, H, lane);
       tgather_lin<3>(a.txo, H, T + P_XO, xs, a, &fail_s);
       mark(a, s, 4 + 5 * l);
-      // With head attention the attention-output wait comes right after QKV,
-      // so the last gate/up slot is not issued with slots 1-3; issued before
-      // the X_o wait it held that wait 1.3 us, so it goes out after it, and
-      // its dots come last: the first four slots' dots cover its round trip.
-      if (HA) issue_gu(l, true, 4);
+      // The last gate/up slot goes out only now: issued with slots 1-3 (or,
+      // with head attention, before the X_o wait) it held the waits behind it
+      // (the X_o wait 1.3 us with head attention). Its dots come last, so the
+      // first four slots' dots cover its round trip.
+      issue_gu(l, true, 4);
       // every dot first, then the stores
       float gy[GPMAX][2];
       {
