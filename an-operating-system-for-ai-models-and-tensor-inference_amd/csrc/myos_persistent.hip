@@ -634,7 +634,9 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
   //   after the items of l (before the merge): gate/up slots 1-3 of l
   //   after the X_o wait of l:                 gate/up slot 4 of l
   //   during gate/up(l), after slot 0's dots:  gate/up slot 0 of l+1
-  //   after the down partials of l:            QKV(l+1), o(l+1)
+  //   after the gate/up dots of l:             o(l+1) with head attention
+  //   after the down partials of l:            QKV(l+1) (and o(l+1) in the
+  //                                            item modes)
   // A wave that issues more loads than its memory queue holds stalls at the
   // issue, so big batches go out where the wave would wait anyway. Loads into
   // LDS make the compiler wait for them before the wave's next LDS access,
@@ -1358,6 +1360,13 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
           if (p == 0 && l + 1 < a.L) issue_gu(l + 1, true, 0);
         }
       }
+      // the next layer's o row, with head attention: issued after the
+      // residual publish it queued ahead of the x wait; here its round trip
+      // passes while the partials are computed and gathered (92.1-92.4 ->
+      // 91.2-91.7 ms per S1 launch; issued between the slots' dots it cost
+      // 0.7-5 ms). The item modes keep it after the publish: here it cost the
+      // long-context launch 204.3-204.7 -> 205.9-206.6 ms.
+      if (HA && l + 1 < a.L) issue_o(l + 1, true);
       // this workgroup's h values, local index wave + p NW, land in LDS; lane
       // p takes slot p, so a wave evaluates one SwiGLU instead of GPMAX in a row
       float *hs = big;
@@ -1443,7 +1452,7 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
       if (l + 1 < a.L) {
         issue_wdp(l + 1, 0);
         issue_q(l + 1, true);
-        issue_o(l + 1, true);
+        if (!HA) issue_o(l + 1, true);
       }
 
     }
