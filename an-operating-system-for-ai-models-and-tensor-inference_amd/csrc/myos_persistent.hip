@@ -641,8 +641,9 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
   // issue, so big batches go out where the wave would wait anyway. Loads into
   // LDS make the compiler wait for them before the wave's next LDS access,
   // so the down block goes in three parts, each just before a wait: before
-  // the x wait of l, after QKV(l) and after o(l). (One batch after QKV(l)
-  // is 9 % slower: the attention-output wait then drains all of it.)
+  // the x wait of l, after QKV(l) (with head attention, between gate/up
+  // slots 2 and 3) and after o(l). (One batch after QKV(l) is 9 % slower:
+  // the attention-output wait then drains all of it.)
   // Layer 0's first share loads after the head, so that no weight row is
   // live across the head's own tiles.
   u32x4 wq0[HC], wq1[HC], wo[HC];
@@ -1104,7 +1105,7 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
         }
       }
 
-      issue_wdp(l, 1);
+      if (!HA) issue_wdp(l, 1);
 
       // ---- attention partials for (kv head, chunk) items (tag T + P_PART) ----
       // (AM 0 and 1; head attention follows below)
@@ -1280,6 +1281,12 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
 
       issue_gu(l, true, 1);
       issue_gu(l, true, 2);
+      // With head attention the down block's second part goes between slots
+      // 2 and 3 rather than ahead of slot 1 (S1 91.3 -> 90.0 ms per launch;
+      // after slot 3 90.2-90.4, after the attention-output wait 99); the item
+      // modes keep it right after QKV (after their slots it cost the
+      // long-context launch 203.4 -> 207.2 ms).
+      if (HA) issue_wdp(l, 1);
       issue_gu(l, true, 3);
 
       // ---- merge: q head h's chunks -> att[h] (tag T + P_ATT), on the last
