@@ -96,12 +96,14 @@ def test_gemv_order_cancellation():
 # the eight-wave 128 x 256 tile unsplit over row tiles with a tail
 # (300, 8960, 512) and for long K in two splits (300, 1280, 4096); the
 # eight-wave 128 x 192 tile for long K when N % 192 == 0, two splits with a
-# row tail (300, 1536, 4096); the single-stage kernel for K % 64 != 0
+# row tail (300, 1536, 4096), and over nine row tiles (1030, 1536, 8960),
+# where the grid of 8 or more M tiles runs in the XCD-aware order with its
+# two splits; the single-stage kernel for K % 64 != 0
 @pytest.mark.parametrize("batch,m,k", [(128, 1536, 1536), (128, 256, 1536), (37, 8960, 1536),
                                        (128, 1536, 8960), (128, 4608, 3584), (100, 17920, 1536),
                                        (1100, 1536, 640), (200, 1536, 8960), (1100, 4096, 256),
                                        (600, 4096, 512), (300, 8960, 512), (300, 1536, 4096),
-                                       (300, 1280, 4096),
+                                       (300, 1280, 4096), (1030, 1536, 8960),
                                        (5, 7, 3), (33, 70, 45), (200, 130, 200)])
 def test_gemm_vs_oracle(batch, m, k):
     rng = np.random.default_rng(batch + m + k)
