@@ -733,7 +733,12 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
 
   // ---- final norm + head + argmax partial of step s (tag tstep + kTPL L);
   // `next` issues the next step's first loads once the head's tiles are out
-  auto head_phase = [&](uint32_t s, uint32_t tstep, auto next) {
+  // pre: the wave's first head tile was issued at the end of the last layer
+  // into the QKV pair's registers (the item modes: the last layer has no
+  // next-layer loads, so the head's first round trip would otherwise start
+  // after the x wait; long-context launch 204.0-204.2 -> 199.6-200.0 ms; with
+  // head attention it cost S1 1.5 %)
+  auto head_phase = [&](uint32_t s, uint32_t tstep, auto next, bool pre) {
     const uint32_t TH = tstep + (uint32_t)a.L * kTPL;
     float bv = -INFINITY;
     uint32_t bi = 0xffffffffu;
@@ -761,8 +766,16 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
       u32x4 ta[HT][HC], tb[HT][HC];
       const int stride = NW * HT;
       int r0 = v0 + wave * HT;
+      if (pre) {
 #pragma unroll
-      for (int r = 0; r < HT; r++) ldrow_all<HC>(ta[r], a.head, H, r0 + r, v1 - 1, lane);
+        for (int i = 0; i < HC; i++) {
+          ta[0][i] = wq0[i];
+          ta[1][i] = wq1[i];
+        }
+      } else {
+#pragma unroll
+        for (int r = 0; r < HT; r++) ldrow_all<HC>(ta[r], a.head, H, r0 + r, v1 - 1, lane);
+      }
       for (; r0 < v1; r0 += 2 * stride) {
         const int r1 = r0 + stride;
 #pragma unroll
@@ -976,7 +989,7 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
         }
         mark(a, s, 2 + 5 * l);
       }
-      head_phase(s, tstep, [&] { att_load_k(0, (int)pos + 1); });
+      head_phase(s, tstep, [&] { att_load_k(0, (int)pos + 1); }, false);
     }
     return;
   }
@@ -1460,11 +1473,15 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
         issue_wdp(l + 1, 0);
         issue_q(l + 1, true);
         if (!HA) issue_o(l + 1, true);
+      } else if (!HA) {
+        // the head's first tile (see head_phase)
+        ldrow_all<HC>(wq0, a.head, H, v0 + wave * HT, v1 - 1, lane);
+        ldrow_all<HC>(wq1, a.head, H, v0 + wave * HT + 1, v1 - 1, lane);
       }
 
     }
 
-    head_phase(s, tstep, [&] { issue_first(0); });
+    head_phase(s, tstep, [&] { issue_first(0); }, !HA);
   }
 
   // ---- hand the state back to the per-kernel path ---------------------------
