@@ -766,6 +766,7 @@ __global__ void __launch_bounds__(NT) decode_persistent_kernel(PersistArgs a) {
       u32x4 ta[HT][HC], tb[HT][HC];
       const int stride = NW * HT;
       int r0 = v0 + wave * HT;
+      static_assert(HT == 2, "the preloaded first tile is the QKV pair's two rows");
       if (pre) {
 #pragma unroll
         for (int i = 0; i < HC; i++) {
