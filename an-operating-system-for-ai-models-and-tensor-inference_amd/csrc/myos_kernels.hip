@@ -2460,6 +2460,10 @@ __global__ void __launch_bounds__(256) attn_prefill_merge_kernel(AttnPrefillArgs
 constexpr int kFsQ = 32;
 constexpr int kFsLds = (4 * kFsQ * (kFaD + 4) + 4 * kFsQ * 2) * (int)sizeof(float);
 
+// KB: the cache holds bf16 (else f32). A compile-time choice: under a run-time
+// flag every V load sat behind its own branch and was waited for where the
+// branch joined, 64 round trips in a row per key block.
+template <bool KB>
 __global__ void __launch_bounds__(256) attn_prefill_small_kernel(AttnPrefillArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t fs_sm[];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -2491,7 +2495,7 @@ __global__ void __launch_bounds__(256) attn_prefill_small_kernel(AttnPrefillArgs
   }
   // 8 consecutive cached values from element offset i (f32 or bf16 cache)
   auto kv8 = [&](const void *base, size_t i, float *v) {
-    if (a.kv_bf16) {
+    if constexpr (KB) {
       const uint4 w = *(const uint4 *)((const uint16_t *)base + i);
       const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
@@ -2505,7 +2509,10 @@ __global__ void __launch_bounds__(256) attn_prefill_small_kernel(AttnPrefillArgs
     }
   };
   auto kv1 = [&](const void *base, size_t i) {
-    return a.kv_bf16 ? bf16f(((const uint16_t *)base)[i]) : ((const float *)base)[i];
+    if constexpr (KB)
+      return bf16f(((const uint16_t *)base)[i]);
+    else
+      return ((const float *)base)[i];
   };
   const size_t head_base = (size_t)g * a.max_seq * kFaD;
 
@@ -3277,12 +3284,13 @@ hipError_t launch_attn_prefill(const AttnPrefillArgs &a, hipStream_t s) {
     // at 32 ids or fewer a single wave would carry all the keys, and the
     // key-split kernel, whose four waves stage each block together, stays
     // ahead (1.86 against 1.88 ms)
-    static bool small_attr = false;
-    const void *fn = (const void *)attn_prefill_small_kernel;
-    if (!small_attr) {
+    static bool small_attr[2] = {false, false};
+    const int kb = a.kv_bf16 ? 1 : 0;
+    const void *fn = kb ? (const void *)attn_prefill_small_kernel<true> : (const void *)attn_prefill_small_kernel<false>;
+    if (!small_attr[kb]) {
       hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, kFsLds);
       if (e != hipSuccess) return e;
-      small_attr = true;
+      small_attr[kb] = true;
     }
     AttnPrefillArgs args = a;
     void *params[] = {&args};
