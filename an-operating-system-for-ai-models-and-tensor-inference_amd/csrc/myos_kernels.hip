@@ -1449,7 +1449,9 @@ __device__ __forceinline__ void qkv_pairs(const GemmArgs &a, const float *cs, in
   }
 }
 
-template <class C, int EPI>
+// TAIL: the launch covers the last gridDim.x * BN columns of N (a tail
+// launch after one over the first columns).
+template <class C, int EPI, bool TAIL = false>
 __global__ void __launch_bounds__(C::NTH) gemm_pf_kernel(GemmArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t pf_sm[];
   constexpr int R = C::R;
@@ -1471,7 +1473,8 @@ __global__ void __launch_bounds__(C::NTH) gemm_pf_kernel(GemmArgs a) {
     tn = r / gm;
     tm = 4 * g + (r - tn * gm);
   }
-  const int n0 = tn * C::BN, m0 = tm * C::BM;
+  const int nb = TAIL ? a.N - gx * C::BN : 0;
+  const int n0 = nb + tn * C::BN, m0 = tm * C::BM;
   const int M = a.M, N = a.N, K = a.K;
   const int nks = K >> 6, S = gridDim.z;
   const int ks0 = (int)((long)z * nks / S), ks1 = (int)((long)(z + 1) * nks / S);
@@ -3152,6 +3155,25 @@ int gemm_splits_old(int M, int N, int K) {
   return (ksteps + kps - 1) / kps;
 }
 
+// Gate/up over many rows on the 128 x 256 tile: when the tiles fill some
+// rounds over the CUs and leave a partial round of at most half the CUs, the
+// N tiles that fill whole rounds run in one launch (returned: that many N
+// tiles) and the rest in a tail launch on 128 x 128 tiles, at most one round.
+// 2048 rows of the 1.5B gate/up: 1120 tiles = 4.375 rounds, 243 us ->
+// 1024 tiles (203-207 us), then 192 128 x 128 tiles (30 us), bit-identical.
+// (The tail as 96 x 2 half-K tiles took 28 us and their reduction 7.5.)
+// 0: one launch.
+static int gu_tail_plan(int M, int N, int K) {
+  static_assert(PfW256::BN % PfW128::BN == 0 && PfW256::BM == PfW128::BM, "tail tiles split the wide ones");
+  if (g_force_cfg >= 0 || K <= 0 || (K & 63) || M <= 0 || N % PfW256::BN) return 0;
+  const GemmPlan p = pf_plan(M, N, K);
+  if (p.cfg != 4 || p.splits != 1) return 0;
+  const long mt = (M + PfW256::BM - 1) / PfW256::BM, nt = N / PfW256::BN, tiles = mt * nt;
+  if (tiles <= kCUs || tiles % kCUs == 0) return 0;
+  const long nm = tiles / kCUs * kCUs / mt, tail = mt * (nt - nm);
+  return nm >= 1 && 2 * tail <= kCUs ? (int)nm : 0;
+}
+
 size_t gemm_ws_floats(int M, int N, int K) {
   const GemmPlan p = pf_plan(M, N, K);
   const int sp = std::max(p.cfg >= 0 ? p.splits : 1, gemm_splits_old(M, N, K));
@@ -3169,16 +3191,18 @@ static int gemm_plan_old(GemmArgs &a) {
   return splits;
 }
 
-template <class C, int EPI>
-static hipError_t go_pf(const GemmArgs &a, int splits, hipStream_t s) {
+// gx > 0: a grid gx tiles wide (the first gx tiles of N, or with TAIL the
+// last gx)
+template <class C, int EPI, bool TAIL = false>
+static hipError_t go_pf(const GemmArgs &a, int splits, hipStream_t s, int gx = 0) {
   static bool attr_done = false;
-  const void *fn = (const void *)gemm_pf_kernel<C, EPI>;
+  const void *fn = (const void *)gemm_pf_kernel<C, EPI, TAIL>;
   if (!attr_done) {
     hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS);
     if (e != hipSuccess) return e;
     attr_done = true;
   }
-  dim3 grid(nblk((size_t)a.N, C::BN), nblk((size_t)a.M, C::BM), splits);
+  dim3 grid(gx > 0 ? (unsigned)gx : nblk((size_t)a.N, C::BN), nblk((size_t)a.M, C::BM), splits);
   GemmArgs args = a;
   void *params[] = {&args};
   return hipLaunchKernel(fn, grid, dim3(C::NTH), params, C::LDS, s);
@@ -3248,6 +3272,14 @@ hipError_t launch_gemm_resid_norm(const GemmArgs &args, const uint16_t *g, float
 template <int EPI>
 static hipError_t launch_gemm_epi(const GemmArgs &args, hipStream_t s) {
   GemmArgs a = args;
+  if constexpr (EPI == EPI_GU) {
+    const int nm = gu_tail_plan(a.M, a.N, a.K);
+    if (nm > 0 && pf_ok(a)) {
+      hipError_t e = go_pf<PfW256, EPI_GU>(a, 1, s, nm);
+      if (e != hipSuccess) return e;
+      return go_pf<PfW128, EPI_GU, true>(a, 1, s, (a.N - nm * PfW256::BN) / PfW128::BN);
+    }
+  }
   int splits = 1;
   hipError_t e = gemm_main<EPI>(a, s, &splits);
   if (e != hipSuccess || splits == 1) return e;

@@ -279,6 +279,25 @@ def test_prefill_attention_key_groups(tmp_path, dims, m):
     g.close()
 
 
+# Gate/up over rows whose 128 x 256 tiles fill some rounds over the 256 CUs
+# and leave a partial one: the N tiles of the whole rounds run in one launch,
+# the rest in a tail launch on 128 x 128 tiles. N = 2 x 4352 = 34 wide tiles:
+# 1100 rows (9 M tiles, 306 tiles) -> 28 of them, then 12 narrow N tiles x 9;
+# 1000 rows (8 M tiles, 272) -> 32, then 4 x 8.
+@pytest.mark.parametrize("m", [1000, 1100])
+def test_gate_up_tail_launch(tmp_path, m):
+    s = shape_dict(512, 4, 1, 128, 4352, 2048, 2, 1e-6)
+    t = random_map(s, seed=m + 7, std=0.05)
+    g, o = open_pair(tmp_path, s, t, m + 8)
+    prompt = np.random.default_rng(m).integers(0, s["vocab"], m)
+    g.prefill(prompt)
+    assert o.prefill(prompt) == 0
+    assert max_rel(g.logits(), o.logits()) < 1e-4
+    assert max_rel(g.hidden(), o.hidden()) < 1e-4
+    assert_logits_parity(g.logits(), o.logits(), f"prefill of {m} ids")
+    g.close()
+
+
 # Short prompts with head_dim 128 (33 to 128 ids, at most 256 keys) take the
 # one-launch kernel that gives each wave its own key blocks; a prefill in
 # chunks reaches it with a cache already holding rows (start position > 0),
