@@ -625,23 +625,27 @@ __global__ void __launch_bounds__(kBlock) attn_decode_d128_kernel(AttnDecodeArgs
   const int seq = (int)*a.pos_ptr + 1, t0 = c * CH, n = min(CH, seq - t0);
   if (n <= 0) return;  // past the cursor: the merge takes chunks < seq only
   const size_t row0 = (size_t)g * a.max_seq + t0;
+  // positions past the chunk's end are read at its last row (in range) and
+  // zeroed: unconditional loads go out together, where loads under a lane
+  // branch were each waited for where the branch joined
   float4 kr[4], vr[4];
 #pragma unroll
   for (int u = 0; u < 4; u++) {
     const int t = 8 * wave + 4 * half + u;
-    kr[u] = vr[u] = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (t < n) {
-      const size_t e = (row0 + t) * D + 4 * j4;
-      if (KB) {
-        const uint2 k2 = *(const uint2 *)((const uint16_t *)a.kc + e);
-        const uint2 v2 = *(const uint2 *)((const uint16_t *)a.vc + e);
-        kr[u] = make_float4(bf_lo(k2.x), bf_hi(k2.x), bf_lo(k2.y), bf_hi(k2.y));
-        vr[u] = make_float4(bf_lo(v2.x), bf_hi(v2.x), bf_lo(v2.y), bf_hi(v2.y));
-      } else {
-        kr[u] = *(const float4 *)((const float *)a.kc + e);
-        vr[u] = *(const float4 *)((const float *)a.vc + e);
-      }
+    const size_t e = (row0 + min(t, n - 1)) * D + 4 * j4;
+    float4 kx, vx;
+    if (KB) {
+      const uint2 k2 = *(const uint2 *)((const uint16_t *)a.kc + e);
+      const uint2 v2 = *(const uint2 *)((const uint16_t *)a.vc + e);
+      kx = make_float4(bf_lo(k2.x), bf_hi(k2.x), bf_lo(k2.y), bf_hi(k2.y));
+      vx = make_float4(bf_lo(v2.x), bf_hi(v2.x), bf_lo(v2.y), bf_hi(v2.y));
+    } else {
+      kx = *(const float4 *)((const float *)a.kc + e);
+      vx = *(const float4 *)((const float *)a.vc + e);
     }
+    const float4 zero = make_float4(0.f, 0.f, 0.f, 0.f);
+    kr[u] = t < n ? kx : zero;
+    vr[u] = t < n ? vx : zero;
   }
   float4 q4[kMaxQPerKv];
 #pragma unroll
